@@ -1,0 +1,205 @@
+"""Benchmark of the W4A8 ConvRot QLinear hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 32768 --k 5120 --n 13824] [--no-cpu]
+
+A step is one full W4A8 QLinear over a resident synthetic batch: per-token rotation + int8 quantisation of
+x bf16 [M, K], int4 -> int8 decode of the weight [N, K] (group 128, fp16 scales), int8 MFMA GEMM with the
+fused (acc * xs) * s_ch epilogue writing bf16 [M, N].  Prints ONE JSON line (rank 0):
+  value        int8 TOPS of the whole op = 2*M*N*K / step time
+  roofline     the GEMM kernel: algorithmic int8 ops per launch / its mean duration (HIP events on the stream
+               the kernels run on, inside the timed region) against the dense int8 MFMA peak
+  cpu_baseline the CPU oracle (numpy restatement of the reference's torch CPU path) on a row sample of the
+               same workload, scaled to the whole op; the thread count it used is reported
+Only one GPU is used; --gpus N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "minimax-h3-turbo_amd"), os.path.join(ROOT, "tests", "golden")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA (AMD public figure, no sparsity)
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--m", type=int, default=32768)
+    ap.add_argument("--k", type=int, default=5120)
+    ap.add_argument("--n", type=int, default=13824)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def traffic_from_profiles(kernel: str):
+    """HBM bytes per launch measured by rocprofv3 PMC runs and committed under profiles/ (None if absent)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(m: int, k: int, n: int, rows: int):
+    """Time the CPU oracle (restatement of the reference's torch CPU backend) on `rows` rows of the workload plus
+    one per-call weight decode, and scale to M rows: TOPS = 2MNK / (t_decode + t_rows * M / rows)."""
+    import numpy as np
+
+    import inputs as gi
+    from oracle import qlinear_ref as ref
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads") or 1) for i in threadpool_info()) if threadpool_info() else 1
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    xb = gi.activations(rows, k, seed=0)
+    q, s_rel, s_ch, cb = gi.weight_int4_g128(n, k, seed=0)
+    x = ref.bf16_from_bits(xb)
+    t_dec, t_rows = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        w8 = ref.decode_int8_grid(q, s_rel, "f16", cb, 128)
+        t1 = time.perf_counter()
+        xq, xs = ref.quantize_rows(x, "bf16", 256, "ck")
+        acc = ref.int8_mm_emulated(xq, w8)
+        ref.epilogue(acc, xs, s_ch, "bf16", "ck")
+        t2 = time.perf_counter()
+        t_dec.append(t1 - t0)
+        t_rows.append(t2 - t1)
+    td, tr = sorted(t_dec)[1], sorted(t_rows)[1]
+    total = td + tr * m / rows
+    return {"value": round(2.0 * m * n * k / total / 1e12, 4), "unit": "TOPS", "cores": int(threads), "kind": "port",
+            "sample": f"oracle/qlinear_ref.py on {rows} of {m} rows (K={k}, N={n}) + one per-call weight decode, "
+                      f"median of 3; scaled to {m} rows: decode {td:.2f} s + rows {tr:.2f} s x {m / rows:.0f}",
+            "seconds_for_full_op": round(total, 2)}
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from h3turbo_amd import _lib
+    from h3turbo_amd import qlinear as ql
+    from h3turbo_amd.types import W4A8Weight
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    m, k, n = args.m, args.k, args.n
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(m, k, generator=g, device=dev)
+    idx = torch.randperm(k, generator=g, device=dev)[: round(0.01 * k)]
+    x[:, idx] *= 20
+    x = x.to(torch.bfloat16)
+    q = torch.randint(-128, 128, (n, k // 2), generator=g, dtype=torch.int8, device=dev)
+    s_rel = (torch.rand(n, k // 128, generator=g, device=dev) * 15.0 + 0.875).to(torch.float16)
+    s_ch = torch.rand(n, generator=g, device=dev) * 1e-3 + 1e-4
+    cb = torch.arange(-8, 8, dtype=torch.float32, device=dev)
+    w = W4A8Weight(q, s_rel, s_ch, cb, group_size=128, convrot=256)
+
+    lib = _lib.load()
+    dw = ql._DevWeight(w)
+    xq = torch.empty(m, k, dtype=torch.int8, device=dev)
+    xs = torch.empty(m, 1, dtype=torch.float32, device=dev)
+    w8 = torch.empty(n, k, dtype=torch.int8, device=dev)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    ev = {name: [] for name in ("rq", "dec", "gemm")}
+
+    def step(record: bool):
+        def mark():
+            if record:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record(stream)
+                return e
+            return None
+
+        e0 = mark()
+        _lib.check(lib.h3k_rotate_quant(x.data_ptr(), _lib.BF16, m, k, k, 256, 0, xq.data_ptr(), k, xs.data_ptr(), sp), "rq")
+        e1 = mark()
+        _lib.check(lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(), n, k, 128,
+                                     w8.data_ptr(), k, sp), "decode")
+        e2 = mark()
+        _lib.check(lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, dw.s_ch.data_ptr(), None, m, n, k, 0,
+                                     out.data_ptr(), _lib.BF16, n, None, sp), "gemm")
+        e3 = mark()
+        if record:
+            ev["rq"].append((e0, e1))
+            ev["dec"].append((e1, e2))
+            ev["gemm"].append((e2, e3))
+
+    # the step must equal the public API's result
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ql.linear(x, w)), "bench step differs from qlinear.linear"
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed * 1e3 / args.steps
+
+    def mean_ms(pairs):
+        return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+
+    t_rq, t_dec, t_gemm = mean_ms(ev["rq"]), mean_ms(ev["dec"]), mean_ms(ev["gemm"])
+    ops = 2.0 * m * n * k
+    tops = ops / (ms_step * 1e-3) / 1e12
+    gemm_tops = ops / (t_gemm * 1e-3) / 1e12
+    rq_bytes = 2 * m * k + m * k + 4 * m
+    dec_bytes = n * k // 2 + n * (k // 128) * 2 + n * k
+    line = {
+        "metric": "int8 TOPS (% MFMA peak) for W4A8 QLinear at M=32768; H3 DiT block ms",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"W4A8 ConvRot QLinear M={m} K={k} N={n}: bf16 x (1% outlier channels x20), int4 weight "
+                               "group 128 fp16 scales, block-Hadamard 256, bf16 out",
+                   "m": m, "k": k, "n": n, "group": 128, "convrot": 256},
+        "pct_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles("gemm_a8w8"),
+                     "kernel": "gemm_a8w8_kernel", "kernel_ms": round(t_gemm, 4)},
+        "kernels": {
+            "rotate_quant": {"ms": round(t_rq, 4), "GB/s": round(rq_bytes / (t_rq * 1e-3) / 1e9, 1),
+                             "frac_hbm": round(rq_bytes / (t_rq * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "decode_w4": {"ms": round(t_dec, 4), "GB/s": round(dec_bytes / (t_dec * 1e-3) / 1e9, 1),
+                          "frac_hbm": round(dec_bytes / (t_dec * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "gemm_a8w8": {"ms": round(t_gemm, 4), "TOPS": round(gemm_tops, 1)},
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(m, k, n, args.cpu_rows)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

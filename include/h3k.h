@@ -1,0 +1,109 @@
+/*
+ * h3k -- MI355X (gfx950) kernels of the W4A8 ConvRot quantised-linear path, behind a plain C ABI.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer owned by the caller unless stated otherwise.
+ *   - `stream` is a hipStream_t passed as void*; all work is stream-ordered, no entry point synchronises.
+ *   - Return 0 on success, a negative H3K_E* code on failure; h3k_last_error() then names the problem
+ *     (thread-local, valid until the next failing call on the same thread).
+ *   - Strides (ld*) are in ELEMENTS of the pointed-to type (bytes for int8 data).
+ *   - Nothing allocates device memory: scratch is a caller workspace sized by the matching *_workspace call.
+ *
+ * Numerics follow the reference's portable torch backend, quant_mode "ck" (default) or "eager".
+ */
+#ifndef H3K_H
+#define H3K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element type codes */
+#define H3K_BF16 0
+#define H3K_F16 1
+#define H3K_F32 2
+#define H3K_FP8E4M3 3 /* OCP E4M3FN bytes (scales only) */
+
+/* quant modes */
+#define H3K_MODE_CK 0    /* absmax of the unrounded fp32 rotation; epilogue (acc*xs)*s_ch */
+#define H3K_MODE_EAGER 1 /* absmax of the dtype-rounded rotation; epilogue acc*(xs*s_ch) */
+
+/* error codes */
+#define H3K_OK 0
+#define H3K_EINVAL -1   /* bad shape / dtype / alignment / option */
+#define H3K_ELAUNCH -2  /* a HIP runtime call or kernel launch failed */
+#define H3K_ESPACE -3   /* workspace too small */
+
+/* ABI version (bumped on any signature change). */
+int h3k_version(void);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* h3k_last_error(void);
+
+/*
+ * Block-Hadamard rotation + per-token int8 quantisation.
+ * Replaces h3turbo/h3/qlinear.py:295-303 (quantize_activation) and :267-292 (_quantize_rows).
+ *   x   [rows, k] of x_dtype (H3K_BF16 | H3K_F16 | H3K_F32), row stride ldx elements
+ *   rot rotation block, a power of 4 in [4, 1024] dividing k
+ *   q   int8 [rows, k] out, row stride ldq bytes;  xs float32 [rows] out (the per-row scale)
+ */
+int h3k_rotate_quant(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot, int mode,
+                     int8_t* q, int64_t ldq, float* xs, void* stream);
+
+/*
+ * Block-Hadamard rotation only: y = round_to_dtype(fp32(x @ H)) per `rot` block, y has x's dtype.
+ * Replaces h3turbo/h3/qlinear.py:118-132 (rotate) for bf16/f16/f32 inputs.
+ */
+int h3k_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot, void* y, int64_t ldy,
+               void* stream);
+
+/*
+ * int4 codebook indices -> exact int8 grid: clamp(rint(codebook[nib] * s_rel[n, k/group]), -127, 127).
+ * Replaces h3turbo/h3/qlinear.py:194-204 (decode_int8_grid) and :157-191 (_pair_lut/_decode_rows).
+ *   q      packed [n, k/2] bytes, low nibble = even k, row stride ldq bytes (8-byte aligned)
+ *   s_rel  [n, k/group] of s_dtype (H3K_FP8E4M3 | H3K_F16 | H3K_BF16 | H3K_F32), row stride lds elements
+ *   codebook float32 [16] (device)
+ *   w8     int8 [n, k] out, row stride ldw bytes (16-byte aligned)
+ */
+int h3k_decode_w4(const void* q, int64_t ldq, const void* s_rel, int s_dtype, int64_t lds, const float* codebook,
+                  int64_t n, int64_t k, int group, int8_t* w8, int64_t ldw, void* stream);
+
+/*
+ * int8 x int8 -> int32 GEMM (TN: both operands K-contiguous) on int8 MFMA with the fused epilogue
+ *   ck   : out = round(f32(f32(acc) * xs[m]) * s_ch[n])
+ *   eager: out = round(f32(acc) * f32(xs[m] * s_ch[n]))
+ *   bias : out = round(f32(out) + f32(bias[n]))  (bias already in out_dtype; NULL for none)
+ * Replaces h3turbo/h3/qlinear.py:236-254 (_int8_mm) and :396-405 (_TorchRunner._a8 epilogue).
+ *   a [m, k] int8 (lda bytes), w8 [n, k] int8 (ldw bytes), out [m, n] of out_dtype (ldo elements)
+ *   acc_out optional int32 [m, n] (ld n) copy of the exact accumulators (NULL to skip)
+ */
+int h3k_gemm_a8w8(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
+                  const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out, int out_dtype, int64_t ldo,
+                  int32_t* acc_out, void* stream);
+
+/*
+ * The whole W4A8 ConvRot linear: rotate+quantise x, decode the weight, GEMM + epilogue.
+ * Fills the slot of comfy_kitchen's w4a8_int8_linear call, h3turbo/h3/qlinear.py:427-429 (_run_ck).
+ * workspace: device scratch of at least h3k_w4a8_linear_workspace(m, n, k) bytes, 256-byte aligned.
+ */
+size_t h3k_w4a8_linear_workspace(int64_t m, int64_t n, int64_t k);
+int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* q, int64_t ldq,
+                    const void* s_rel, int s_dtype, int64_t lds, const float* s_ch, const float* codebook, int64_t n,
+                    int group, int rot, const void* bias, int mode, void* out, int out_dtype, int64_t ldo,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Host -> device copy of one weight block on the streaming engine's copy stream (hipMemcpyAsync).
+ * Replaces the slot copy of h3turbo/h3/stream.py:346-354 (_issue: slot.buf.copy_(src, non_blocking)).
+ * src is host memory (page-locked for an asynchronous copy), dst device memory.
+ */
+int h3k_copy_h2d_async(void* dst, const void* src, size_t nbytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* H3K_H */

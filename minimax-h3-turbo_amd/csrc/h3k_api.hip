@@ -1,0 +1,81 @@
+// C ABI glue: error reporting, the fused W4A8 linear entry point and the streaming copy.
+#include "h3k_common.hpp"
+
+namespace h3k {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(H3K_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return H3K_OK;
+}
+
+int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
+                     const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out, int out_dtype, int64_t ldo,
+                     int32_t* acc_out, hipStream_t st);
+
+static inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace h3k
+
+using namespace h3k;
+
+extern "C" int h3k_version(void) { return 1; }
+
+extern "C" const char* h3k_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" size_t h3k_w4a8_linear_workspace(int64_t m, int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k < 0) return 0;
+  return round_up(static_cast<size_t>(m) * k, 256) + round_up(static_cast<size_t>(m) * 4, 256) +
+         round_up(static_cast<size_t>(n) * k, 256);
+}
+
+extern "C" int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* q,
+                               int64_t ldq, const void* s_rel, int s_dtype, int64_t lds, const float* s_ch,
+                               const float* codebook, int64_t n, int group, int rot, const void* bias, int mode,
+                               void* out, int out_dtype, int64_t ldo, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  const size_t need = h3k_w4a8_linear_workspace(m, n, k);
+  if (workspace_bytes < need)
+    return fail(H3K_ESPACE, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  if (m == 0 || n == 0) return H3K_OK;
+  if (!workspace || !aligned(workspace, 256)) return fail(H3K_EINVAL, "workspace must be 256-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  int8_t* aq = reinterpret_cast<int8_t*>(ws);
+  float* xs = reinterpret_cast<float*>(ws + round_up(static_cast<size_t>(m) * k, 256));
+  int8_t* w8 = reinterpret_cast<int8_t*>(ws + round_up(static_cast<size_t>(m) * k, 256) + round_up(static_cast<size_t>(m) * 4, 256));
+  int rc = h3k_rotate_quant(x, x_dtype, m, k, ldx, rot, mode, aq, k, xs, stream);
+  if (rc) return rc;
+  rc = h3k_decode_w4(q, ldq, s_rel, s_dtype, lds, codebook, n, k, group, w8, k, stream);
+  if (rc) return rc;
+  return gemm_a8w8_launch(aq, k, xs, w8, k, s_ch, bias, m, n, k, mode, out, out_dtype, ldo, nullptr,
+                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int h3k_copy_h2d_async(void* dst, const void* src, size_t nbytes, void* stream) {
+  if (nbytes == 0) return H3K_OK;
+  if (!dst || !src) return fail(H3K_EINVAL, "NULL pointer");
+  const hipError_t e = hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(H3K_ELAUNCH, "hipMemcpyAsync: %s", hipGetErrorString(e));
+  return H3K_OK;
+}

@@ -1,0 +1,206 @@
+// int8 x int8 -> int32 GEMM on CDNA4 int8 MFMA (v_mfma_i32_32x32x32_i8) with the W4A8 epilogue fused.
+//
+//   acc[m, n] = sum_k a[m, k] * w8[n, k]                         exact int32 (|acc| < 2^31 for k < 130k)
+//   ck   : out = round(f32(f32(acc) * xs[m]) * s_ch[n])          reference h3turbo/h3/qlinear.py:401
+//   eager: out = round(f32(acc) * f32(xs[m] * s_ch[n]))          reference h3turbo/h3/qlinear.py:403
+//   bias : out = round(f32(out) + f32(bias[n]))                  reference h3turbo/h3/qlinear.py:404-405
+//
+// Tiling: a 256-thread workgroup (2 x 2 wavefronts) owns a BM x BN output tile; each wavefront owns
+// (BM/2) x (BN/2) as WMB x WNB MFMA 32x32 blocks held in accumulation registers.  K advances 64 bytes per
+// step through double-buffered LDS tiles (row-major, 64 B per row, 16-byte chunks XOR-swizzled by row so both
+// the 16-byte global->LDS stores and the 16-byte MFMA fragment reads are bank-conflict free).  Operands that
+// fall outside M, N or K load as zeros; stores are masked.  Workgroup ids are remapped so each XCD works
+// through a contiguous, row-grouped range of tiles (its own L2 then serves the shared A/B panels).
+#include "h3k_common.hpp"
+
+namespace h3k {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 64;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ int swz(int r, int c) { return r * kBK + ((c ^ ((r >> 1) & 3)) << 4); }
+
+// tile id -> (tile_m, tile_n): XCD-contiguous ranges, then groups of kGroupM tile-rows walked column by column
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int per = total >> 3, rem = total & 7;
+  const int id = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int in_group = kGroupM * tiles_n;
+  const int gid = id / in_group;
+  const int first_m = gid * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  const int r = id - gid * in_group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
+
+template <int WMB, int WNB>
+__global__ __launch_bounds__(256, 1) void gemm_a8w8_kernel(const int8_t* __restrict__ A, int64_t lda,
+                                                           const int8_t* __restrict__ B, int64_t ldb, int M, int N, int K,
+                                                           const float* __restrict__ xs, const float* __restrict__ sch,
+                                                           const void* __restrict__ bias, void* __restrict__ out,
+                                                           int64_t ldo, int32_t* __restrict__ acc_out, int mode,
+                                                           int out_dtype) {
+  constexpr int BM = 64 * WMB, BN = 64 * WNB;
+  constexpr int A_LD = BM / 64, B_LD = BN / 64;  // 16-byte chunks per thread per K step
+  __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * kBK];
+  __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * kBK];
+
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  uint4 ra[A_LD], rb[B_LD];
+  auto gload = [&](int kt) {
+    const int kb = kt * kBK;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = tid + 256 * i, r = id >> 2, c = id & 3;
+      const int gr = m0 + r, kk = kb + c * 16;
+      ra[i] = (gr < M && kk < K) ? *reinterpret_cast<const uint4*>(A + static_cast<int64_t>(gr) * lda + kk)
+                                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int id = tid + 256 * i, r = id >> 2, c = id & 3;
+      const int gr = n0 + r, kk = kb + c * 16;
+      rb[i] = (gr < N && kk < K) ? *reinterpret_cast<const uint4*>(B + static_cast<int64_t>(gr) * ldb + kk)
+                                 : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = tid + 256 * i, r = id >> 2, c = id & 3;
+      *reinterpret_cast<uint4*>(&sA[buf][swz(r, c)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int id = tid + 256 * i, r = id >> 2, c = id & 3;
+      *reinterpret_cast<uint4*>(&sB[buf][swz(r, c)]) = rb[i];
+    }
+  };
+
+  v16i acc[WMB][WNB];
+#pragma unroll
+  for (int i = 0; i < WMB; ++i)
+#pragma unroll
+    for (int j = 0; j < WNB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int KT = (K + kBK - 1) / kBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int arow = wm * (32 * WMB) + (lane & 31), brow = wn * (32 * WNB) + (lane & 31), kh = lane >> 5;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      v4i af[WMB], bf[WNB];
+      const int c = s * 2 + kh;
+#pragma unroll
+      for (int i = 0; i < WMB; ++i) af[i] = *reinterpret_cast<const v4i*>(&sA[cur][swz(arow + i * 32, c)]);
+#pragma unroll
+      for (int j = 0; j < WNB; ++j) bf[j] = *reinterpret_cast<const v4i*>(&sB[cur][swz(brow + j * 32, c)]);
+#pragma unroll
+      for (int i = 0; i < WMB; ++i)
+#pragma unroll
+        for (int j = 0; j < WNB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  // C layout of a 32x32 MFMA block: lane l holds column (l % 32); register r holds row
+  // (r / 4) * 8 + (l / 32) * 4 + (r % 4).
+  const bool eager = mode == H3K_MODE_EAGER;
+#pragma unroll
+  for (int j = 0; j < WNB; ++j) {
+    const int gn = n0 + wn * (32 * WNB) + j * 32 + (lane & 31);
+    if (gn >= N) continue;
+    const float sc = sch[gn];
+    float bv = 0.0f;
+    if (bias) {
+      if (out_dtype == H3K_F32) bv = static_cast<const float*>(bias)[gn];
+      else if (out_dtype == H3K_F16) bv = f16_to_f32(static_cast<const uint16_t*>(bias)[gn]);
+      else bv = bf16_to_f32(static_cast<const uint16_t*>(bias)[gn]);
+    }
+#pragma unroll
+    for (int i = 0; i < WMB; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + wm * (32 * WMB) + i * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+        if (gm >= M) continue;
+        const int a = acc[i][j][r];
+        if (acc_out) acc_out[static_cast<int64_t>(gm) * N + gn] = a;
+        const float xv = xs[gm];
+        float f = eager ? static_cast<float>(a) * (xv * sc) : (static_cast<float>(a) * xv) * sc;
+        const int64_t o = static_cast<int64_t>(gm) * ldo + gn;
+        if (out_dtype == H3K_F32) {
+          if (bias) f = f + bv;
+          static_cast<float*>(out)[o] = f;
+        } else if (out_dtype == H3K_F16) {
+          f = round_f16(f);
+          if (bias) f = f + bv;
+          static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_f16_bits(f));
+        } else {
+          f = round_bf16(f);
+          if (bias) f = f + bv;
+          static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_bf16_bits(f));
+        }
+      }
+    }
+  }
+}
+
+template <int WMB, int WNB>
+static void launch_gemm(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k, const float* xs,
+                        const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, int mode, int odt,
+                        hipStream_t st) {
+  constexpr int BM = 64 * WMB, BN = 64 * WNB;
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_a8w8_kernel<WMB, WNB>), dim3(tiles), dim3(256), 0, st, a, lda, b, ldb, m, n, k, xs, sch, bias,
+                     out, ldo, acc, mode, odt);
+}
+
+int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
+                     const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out, int out_dtype, int64_t ldo,
+                     int32_t* acc_out, hipStream_t st) {
+  if (m < 0 || n < 0 || k < 0 || m > (1 << 30) || n > (1 << 30) || k > (1 << 17))
+    return fail(H3K_EINVAL, "bad GEMM shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  if (k % 16) return fail(H3K_EINVAL, "k=%lld must be a multiple of 16", (long long)k);
+  if (mode != H3K_MODE_CK && mode != H3K_MODE_EAGER) return fail(H3K_EINVAL, "mode must be ck (0) or eager (1)");
+  if (out_dtype != H3K_BF16 && out_dtype != H3K_F16 && out_dtype != H3K_F32)
+    return fail(H3K_EINVAL, "out dtype code %d unsupported", out_dtype);
+  if (lda < k || ldw < k || ldo < n) return fail(H3K_EINVAL, "row strides smaller than the rows");
+  if (m == 0 || n == 0) return H3K_OK;
+  if (!a || !xs || !w8 || !s_ch || !out) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(a, 16) || lda % 16 || !aligned(w8, 16) || ldw % 16)
+    return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
+  const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
+  if (m >= 2048 && n >= 256)
+    launch_gemm<4, 4>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
+  else
+    launch_gemm<2, 2>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
+  return check_launch("gemm_a8w8");
+}
+
+}  // namespace h3k
+
+extern "C" int h3k_gemm_a8w8(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw,
+                             const float* s_ch, const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out,
+                             int out_dtype, int64_t ldo, int32_t* acc_out, void* stream) {
+  return h3k::gemm_a8w8_launch(a, lda, xs, w8, ldw, s_ch, bias, m, n, k, mode, out, out_dtype, ldo, acc_out,
+                               static_cast<hipStream_t>(stream));
+}

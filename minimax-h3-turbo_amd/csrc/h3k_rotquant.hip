@@ -1,0 +1,359 @@
+// Block-Hadamard (ConvRot) rotation + per-token int8 quantisation for gfx950.
+//
+// Numerics (reference h3turbo/h3/qlinear.py:105-115, 267-292, quant_mode "ck"/"eager"):
+//   y32[j] = fp32( sum_i x[i] * H[i, j] )       H = kron(H4, ..., H4) / sqrt(rot), exact dyadic entries
+//   amax   = max_j |y32[j]|   ("ck")   or   max_j |round_dtype(y32[j])|   ("eager")
+//   xs     = max(amax / 127, 1e-30)                                   (fp32, returned)
+//   s      = round_dtype(xs), 0 -> finfo(dtype).tiny
+//   q[j]   = clamp(rint_half_even(round_dtype(round_dtype(y32[j]) / s)), -128, 127)
+// The rotation is a fast Walsh-Hadamard transform in float64: the products are exact (entries +-2^-p) and
+// every partial sum of <= 1024 bf16 / f16 terms is exact in fp64 unless a block spans more than ~2^37 in
+// magnitude, so the single rounding to fp32 reproduces the reference's fp64 matmul bit for bit.
+//
+// Fast path (rot = 256, bf16/f16): one wavefront per row, 4 rows per 256-thread workgroup.  A 256-block spans
+// 16 lanes x 16 elements; the four base-4 digits of the in-block index are brought into registers two at a
+// time by two LDS transposes (bf16 input, then fp64 mid-values), so every butterfly is register-local.  The
+// whole row stays in registers as rounded 16-bit values until its absmax is known; x is read once and q
+// written once.
+#include "h3k_common.hpp"
+
+namespace h3k {
+
+// y = x @ H4 on four values (H4 symmetric): (s - 2d, s - 2c, s - 2b, s - 2a) with s = a + b + c + d.
+__device__ __forceinline__ void h4(double& a, double& b, double& c, double& d) {
+  const double s = (a + b) + (c + d);
+  const double na = fma(d, -2.0, s), nb = fma(c, -2.0, s), nc = fma(b, -2.0, s), nd = fma(a, -2.0, s);
+  a = na;
+  b = nb;
+  c = nc;
+  d = nd;
+}
+
+// Same, folding the final 1/16 of H256 in: every operation stays exact (power-of-two scaling).
+__device__ __forceinline__ void h4_div16(double& a, double& b, double& c, double& d) {
+  const double s = ((a + b) + (c + d)) * 0.0625;
+  const double na = fma(d, -0.125, s), nb = fma(c, -0.125, s), nc = fma(b, -0.125, s), nd = fma(a, -0.125, s);
+  a = na;
+  b = nb;
+  c = nc;
+  d = nd;
+}
+
+template <bool F16>
+__device__ __forceinline__ float to_f32_16(uint32_t bits) {
+  return F16 ? f16_to_f32(bits) : bf16_to_f32(bits);
+}
+template <bool F16>
+__device__ __forceinline__ uint32_t round_bits_16(float f) {
+  return F16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+}
+
+// LDS geometry of the fast path (per wave, per 16-lane group g)
+constexpr int kInStride = 16 * 16 + 16;  // uint16 per group: 16 rows of 16 + pad (skews groups by 8 banks)
+constexpr int kMidRow = 17;              // doubles per mid-transpose row (odd: conflict-free 64-bit access)
+constexpr int kMidStride = 16 * kMidRow + 4;
+
+template <int NPASS, bool F16, bool EAGER>
+__global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __restrict__ x, int64_t rows, int k,
+                                                          int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
+                                                          float* __restrict__ xs) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_in[4][4 * kInStride];
+  __shared__ __attribute__((aligned(16))) double s_mid[4][4 * kMidStride];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (row >= rows) return;
+  const int g = lane >> 4, l = lane & 15;
+  const int nb = k >> 8;
+  const uint16_t* xr = x + row * ldx;
+
+  u32x4 raw[NPASS][2];
+#pragma unroll
+  for (int p = 0; p < NPASS; ++p) {
+    const int b = p * 4 + g;
+    if (b < nb) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(xr + b * 256 + l * 16);
+      raw[p][0] = __builtin_nontemporal_load(src);
+      raw[p][1] = __builtin_nontemporal_load(src + 1);
+    } else {
+      raw[p][0] = u32x4{0, 0, 0, 0};
+      raw[p][1] = u32x4{0, 0, 0, 0};
+    }
+  }
+
+  uint16_t* tin = &s_in[wave][g * kInStride];
+  double* tmid = &s_mid[wave][g * kMidStride];
+  uint32_t yb[NPASS][8];  // rounded rotation, two 16-bit values per word, contiguous elements l*16 ..
+  float amax = 0.0f;
+
+#pragma unroll
+  for (int p = 0; p < NPASS; ++p) {
+    const bool live = (p * 4 + g) < nb;
+    // (1) transpose the 16-bit input: lane l then holds elements l + 16*r, r = 0..15 (digits 2,3 local)
+    wave_lds_sync();
+    *reinterpret_cast<u32x4*>(tin + l * 16) = raw[p][0];
+    *reinterpret_cast<u32x4*>(tin + l * 16 + 8) = raw[p][1];
+    wave_lds_sync();
+    double v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = static_cast<double>(to_f32_16<F16>(tin[r * 16 + l]));
+    // (2) digit 2 (r = d2 + 4*d3) and digit 3
+#pragma unroll
+    for (int d3 = 0; d3 < 4; ++d3) h4(v[4 * d3], v[4 * d3 + 1], v[4 * d3 + 2], v[4 * d3 + 3]);
+#pragma unroll
+    for (int d2 = 0; d2 < 4; ++d2) h4(v[d2], v[d2 + 4], v[d2 + 8], v[d2 + 12]);
+    // (3) transpose the fp64 mid-values back: lane l then holds elements 16*l + j, j = 0..15 (digits 0,1 local)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tmid[r * kMidRow + l] = v[r];
+    wave_lds_sync();
+    double w[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) w[j] = tmid[l * kMidRow + j];
+    // (4) digit 0 (j = d0 + 4*d1), then digit 1 with the 1/16 folded in
+#pragma unroll
+    for (int d1 = 0; d1 < 4; ++d1) h4(w[4 * d1], w[4 * d1 + 1], w[4 * d1 + 2], w[4 * d1 + 3]);
+#pragma unroll
+    for (int d0 = 0; d0 < 4; ++d0) h4_div16(w[d0], w[d0 + 4], w[d0 + 8], w[d0 + 12]);
+    // (5) one rounding to fp32, absmax, one rounding to the activation dtype
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      const float y0 = static_cast<float>(w[j]), y1 = static_cast<float>(w[j + 1]);
+      const uint32_t b0 = round_bits_16<F16>(y0), b1 = round_bits_16<F16>(y1);
+      if (live) {
+        if (EAGER) {
+          amax = fmaxf(amax, fmaxf(fabsf(to_f32_16<F16>(b0)), fabsf(to_f32_16<F16>(b1))));
+        } else {
+          amax = fmaxf(amax, fmaxf(fabsf(y0), fabsf(y1)));
+        }
+      }
+      yb[p][j >> 1] = b0 | (b1 << 16);
+    }
+  }
+
+  amax = wave_max(amax);
+  const float xsv = fmaxf(amax / 127.0f, 1e-30f);
+  if (lane == 0) xs[row] = xsv;
+  float s = F16 ? round_f16(xsv) : round_bf16(xsv);
+  if (s == 0.0f) s = F16 ? 6.103515625e-05f : 1.1754943508222875e-38f;
+  // bf16: bf16(y * fl(1/s)) == bf16(fl(y / s)) for bf16 y, s (8-bit mantissas; checked exhaustively on the CPU)
+  const float rs = 1.0f / s;
+
+  int8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int p = 0; p < NPASS; ++p) {
+    const int b = p * 4 + g;
+    if (b >= nb) continue;
+    uint32_t packed[4];
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = w4 * 4 + e;
+        const uint32_t bits = (yb[p][j >> 1] >> ((j & 1) * 16)) & 0xFFFFu;
+        const float y = to_f32_16<F16>(bits);
+        float t;
+        if (F16) {
+          t = round_f16(y / s);
+        } else {
+          t = round_bf16(y * rs);
+        }
+        t = __builtin_rintf(t);
+        t = __builtin_amdgcn_fmed3f(t, -128.0f, 127.0f);
+        word |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xFFu) << (8 * e);
+      }
+      packed[w4] = word;
+    }
+    __builtin_nontemporal_store(u32x4{packed[0], packed[1], packed[2], packed[3]},
+                                reinterpret_cast<u32x4*>(qr + b * 256 + l * 16));
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ generic path
+// One 256-thread workgroup per row; the row is processed in chunks of 1024 staged in LDS as float64 and
+// transformed stage by stage.  Two sweeps: absmax, then quantise (or store the rounded rotation).
+template <int DT>
+__device__ __forceinline__ float load_x(const void* x, int64_t idx) {
+  if (DT == H3K_F32) return static_cast<const float*>(x)[idx];
+  const uint32_t bits = static_cast<const uint16_t*>(x)[idx];
+  return DT == H3K_F16 ? f16_to_f32(bits) : bf16_to_f32(bits);
+}
+template <int DT>
+__device__ __forceinline__ float round_dt(float f) {
+  if (DT == H3K_F32) return f;
+  return DT == H3K_F16 ? round_f16(f) : round_bf16(f);
+}
+
+template <int DT, bool EAGER, bool ROTATE_ONLY>
+__global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict__ x, int64_t rows, int k, int64_t ldx,
+                                                          int log4, int8_t* __restrict__ q, int64_t ldq,
+                                                          float* __restrict__ xs, void* __restrict__ y, int64_t ldy) {
+  __shared__ double buf[1024];
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  const int t = threadIdx.x;
+  const double scale = ldexp(1.0, -log4);  // 1/sqrt(4^log4), exact
+  float amax = 0.0f, s = 1.0f;
+
+  for (int sweep = ROTATE_ONLY ? 1 : 0; sweep < 2; ++sweep) {
+    for (int c0 = 0; c0 < k; c0 += 1024) {
+      const int n = min(1024, k - c0);
+      __syncthreads();
+      for (int e = t; e < n; e += 256) buf[e] = static_cast<double>(load_x<DT>(x, row * ldx + c0 + e));
+      __syncthreads();
+      for (int d = 0, S = 1; d < log4; ++d, S *= 4) {
+        const int base = (t / S) * 4 * S + (t % S);
+        if (base < n) h4(buf[base], buf[base + S], buf[base + 2 * S], buf[base + 3 * S]);
+        __syncthreads();
+      }
+      for (int e = t; e < n; e += 256) {
+        const float y32 = static_cast<float>(buf[e] * scale);
+        const float yr = round_dt<DT>(y32);
+        if (sweep == 0) {
+          amax = fmaxf(amax, fabsf(EAGER ? yr : y32));
+        } else if (ROTATE_ONLY) {
+          if (DT == H3K_F32) {
+            static_cast<float*>(y)[row * ldy + c0 + e] = yr;
+          } else {
+            const uint32_t bits = DT == H3K_F16 ? f32_to_f16_bits(y32) : f32_to_bf16_bits(y32);
+            static_cast<uint16_t*>(y)[row * ldy + c0 + e] = static_cast<uint16_t>(bits);
+          }
+        } else {
+          float tq = (DT == H3K_F32) ? (yr / s) : round_dt<DT>(yr / s);
+          tq = __builtin_amdgcn_fmed3f(__builtin_rintf(tq), -128.0f, 127.0f);
+          q[row * ldq + c0 + e] = static_cast<int8_t>(static_cast<int>(tq));
+        }
+      }
+    }
+    if (sweep == 0) {
+      amax = wave_max(amax);
+      if ((t & 63) == 0) red[t >> 6] = amax;
+      __syncthreads();
+      amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+      const float xsv = fmaxf(amax / 127.0f, 1e-30f);
+      if (t == 0) xs[row] = xsv;
+      s = round_dt<DT>(xsv);
+      if (s == 0.0f) s = DT == H3K_F16 ? 6.103515625e-05f : 1.1754943508222875e-38f;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ host side
+template <int NPASS, bool F16, bool EAGER>
+static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int8_t* q, int64_t ldq, float* xs,
+                      hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  hipLaunchKernelGGL((rotquant256_kernel<NPASS, F16, EAGER>), grid, dim3(256), 0, st,
+                     static_cast<const uint16_t*>(x), rows, k, ldx, q, ldq, xs);
+}
+
+template <bool F16, bool EAGER>
+static bool dispatch256(int npass, const void* x, int64_t rows, int k, int64_t ldx, int8_t* q, int64_t ldq, float* xs,
+                        hipStream_t st) {
+  switch (npass) {
+#define H3K_CASE(P) \
+  case P:           \
+    launch256<P, F16, EAGER>(x, rows, k, ldx, q, ldq, xs, st); \
+    return true;
+    H3K_CASE(1) H3K_CASE(2) H3K_CASE(3) H3K_CASE(4) H3K_CASE(5) H3K_CASE(6) H3K_CASE(7) H3K_CASE(8)
+    H3K_CASE(10) H3K_CASE(12) H3K_CASE(14) H3K_CASE(16)
+#undef H3K_CASE
+    default:
+      return false;
+  }
+}
+
+static int npass_bucket(int blocks) {
+  const int need = (blocks + 3) / 4;
+  static const int buckets[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
+  for (int b : buckets)
+    if (b >= need) return b;
+  return 0;
+}
+
+static int check_rot_args(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot) {
+  if (x_dtype != H3K_BF16 && x_dtype != H3K_F16 && x_dtype != H3K_F32)
+    return fail(H3K_EINVAL, "activations must be bf16, f16 or f32 (dtype code %d)", x_dtype);
+  if (!is_pow4(rot)) return fail(H3K_EINVAL, "rotation block must be a power of 4 in [4, 1024], got %d", rot);
+  if (rows < 0 || k <= 0 || k % rot) return fail(H3K_EINVAL, "k=%lld must be a positive multiple of the rotation block %d", (long long)k, rot);
+  if (k > (1 << 30)) return fail(H3K_EINVAL, "k=%lld too large", (long long)k);
+  if (ldx < k) return fail(H3K_EINVAL, "ldx=%lld < k=%lld", (long long)ldx, (long long)k);
+  if (rows > 0 && x == nullptr) return fail(H3K_EINVAL, "x is NULL");
+  return H3K_OK;
+}
+
+static int log4_of(int rot) {
+  int l = 0;
+  while (rot > 1) {
+    rot >>= 2;
+    ++l;
+  }
+  return l;
+}
+
+}  // namespace h3k
+
+using namespace h3k;
+
+extern "C" int h3k_rotate_quant(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot, int mode,
+                                int8_t* q, int64_t ldq, float* xs, void* stream) {
+  int rc = check_rot_args(x, x_dtype, rows, k, ldx, rot);
+  if (rc) return rc;
+  if (mode != H3K_MODE_CK && mode != H3K_MODE_EAGER) return fail(H3K_EINVAL, "mode must be ck (0) or eager (1)");
+  if (ldq < k) return fail(H3K_EINVAL, "ldq=%lld < k=%lld", (long long)ldq, (long long)k);
+  if (rows == 0) return H3K_OK;
+  if (!q || !xs) return fail(H3K_EINVAL, "q/xs is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool eager = mode == H3K_MODE_EAGER;
+  const int es = x_dtype == H3K_F32 ? 4 : 2;
+  const bool fast = rot == 256 && x_dtype != H3K_F32 && aligned(x, 16) && (ldx * es) % 16 == 0 && aligned(q, 16) &&
+                    ldq % 16 == 0 && npass_bucket(static_cast<int>(k / 256)) > 0;
+  if (fast) {
+    const int np = npass_bucket(static_cast<int>(k / 256));
+    const int kk = static_cast<int>(k);
+    bool ok;
+    if (x_dtype == H3K_F16)
+      ok = eager ? dispatch256<true, true>(np, x, rows, kk, ldx, q, ldq, xs, st)
+                 : dispatch256<true, false>(np, x, rows, kk, ldx, q, ldq, xs, st);
+    else
+      ok = eager ? dispatch256<false, true>(np, x, rows, kk, ldx, q, ldq, xs, st)
+                 : dispatch256<false, false>(np, x, rows, kk, ldx, q, ldq, xs, st);
+    if (!ok) return fail(H3K_EINVAL, "no fast rotation kernel for k=%lld", (long long)k);
+    return check_launch("rotquant256");
+  }
+  const dim3 grid(static_cast<unsigned>(rows));
+  const int l4 = log4_of(rot), kk = static_cast<int>(k);
+#define H3K_GEN(DT, E) \
+  hipLaunchKernelGGL((rot_generic_kernel<DT, E, false>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4, q, ldq, xs, nullptr, 0)
+  if (x_dtype == H3K_BF16) {
+    if (eager) H3K_GEN(H3K_BF16, true); else H3K_GEN(H3K_BF16, false);
+  } else if (x_dtype == H3K_F16) {
+    if (eager) H3K_GEN(H3K_F16, true); else H3K_GEN(H3K_F16, false);
+  } else {
+    if (eager) H3K_GEN(H3K_F32, true); else H3K_GEN(H3K_F32, false);
+  }
+#undef H3K_GEN
+  return check_launch("rot_generic(quant)");
+}
+
+extern "C" int h3k_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot, void* y,
+                          int64_t ldy, void* stream) {
+  int rc = check_rot_args(x, x_dtype, rows, k, ldx, rot);
+  if (rc) return rc;
+  if (ldy < k) return fail(H3K_EINVAL, "ldy=%lld < k=%lld", (long long)ldy, (long long)k);
+  if (rows == 0) return H3K_OK;
+  if (!y) return fail(H3K_EINVAL, "y is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(rows));
+  const int l4 = log4_of(rot), kk = static_cast<int>(k);
+  if (x_dtype == H3K_BF16)
+    hipLaunchKernelGGL((rot_generic_kernel<H3K_BF16, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4,
+                       nullptr, 0, nullptr, y, ldy);
+  else if (x_dtype == H3K_F16)
+    hipLaunchKernelGGL((rot_generic_kernel<H3K_F16, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4,
+                       nullptr, 0, nullptr, y, ldy);
+  else
+    hipLaunchKernelGGL((rot_generic_kernel<H3K_F32, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4,
+                       nullptr, 0, nullptr, y, ldy);
+  return check_launch("rot_generic(rotate)");
+}

@@ -1,0 +1,352 @@
+"""ConvRot W4A8 linear ops on MI355X: the drop-in for h3turbo/h3/qlinear.py.
+
+Same public surface and error behaviour as the reference module (h3turbo/h3/qlinear.py:44-523):
+`linear`, `quantize_activation`, `rotate`, `decode_int8_grid`, `dequantize`, `hadamard_regular`,
+`available_backends`, `resolve_backend`, with one more backend, "hip", that runs the hand-written gfx950 kernels
+of libh3k.so (include/h3k.h).  "auto" resolves to "hip".  The reference's other backends are not part of this
+build: "ck" (comfy_kitchen CUDA) and "torch" (portable) raise RuntimeError when requested, like the reference
+does for an unusable backend.  Argument errors raise ValueError with the reference's messages before any device
+check; W4A8 compute on CPU tensors raises RuntimeError (the product never falls back to a CPU path).
+
+Numerics (bit-exact with the reference's torch backend, quant_mode "ck" or "eager"):
+  quantize_activation : fp64 Walsh-Hadamard rotation rounded once to fp32, per-row absmax int8
+  decode_int8_grid    : clamp(rint(codebook[nib] * s_rel), +-127)
+  linear (a8)         : exact int32 GEMM on int8 MFMA, (acc * xs) * s_ch rounded once, bias after rounding
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .types import W4A8Weight, Weight
+
+CONVROT = 256
+_H4 = ((1, 1, 1, -1), (1, 1, -1, 1), (1, -1, 1, 1), (-1, 1, 1, 1))
+_HAD_CACHE: Dict[Tuple[int, str, int, torch.dtype], torch.Tensor] = {}
+_BACKENDS = ("auto", "hip", "ck", "torch")
+
+
+# --------------------------------------------------------------------------------------------- Hadamard
+def hadamard_regular(size: int, device="cpu", dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Normalised regular Hadamard H = kron(H4, ..., H4) / sqrt(size); symmetric, H @ H = I (qlinear.py:44-66).
+    Entries are +-2^-j, exact in every float dtype.  Cached: do not mutate the result."""
+    n = size
+    while n > 1 and n % 4 == 0:
+        n //= 4
+    if size < 4 or n != 1:
+        raise ValueError(f"regular Hadamard size must be a power of 4 (>= 4), got {size}")
+    dev = torch.device(device)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    key = (size, dev.type, -1 if dev.index is None else dev.index, dtype)
+    h = _HAD_CACHE.get(key)
+    if h is None:
+        h4 = torch.tensor(_H4, dtype=torch.float32)
+        full = h4
+        for _ in range(round(math.log(size, 4)) - 1):
+            full = torch.kron(full, h4)
+        h = (full / math.sqrt(size)).to(device=dev, dtype=dtype).contiguous()
+        _HAD_CACHE[key] = h
+    return h
+
+
+# --------------------------------------------------------------------------------------------- helpers
+def _need_gpu(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{what}: h3turbo_amd computes W4A8 ops on the GPU (HIP, gfx950) only; got a {t.device} "
+                           "tensor (move it to the ROCm device)")
+
+
+def _rows(x2: torch.Tensor) -> torch.Tensor:
+    """[M, K] view whose last dim is contiguous (the kernels take a row stride)."""
+    return x2 if x2.stride(-1) == 1 and (x2.shape[0] <= 1 or x2.stride(0) >= x2.shape[1]) else x2.contiguous()
+
+
+def _ld(x2: torch.Tensor) -> int:
+    """Row stride of a row-contiguous [M, K] view (any value >= K serves a single row)."""
+    return x2.stride(0) if x2.shape[0] > 1 else x2.shape[1]
+
+
+def _check_mode(mode: str) -> None:
+    if mode not in ("ck", "eager"):
+        raise ValueError(f"quant_mode must be 'ck' or 'eager', got {mode!r}")
+
+
+def _check_weight(w: W4A8Weight) -> Tuple[int, int]:
+    """The reference's weight validation (qlinear.py:140-154), same messages."""
+    if w.q.dim() != 2 or w.q.dtype not in (torch.int8, torch.uint8):
+        raise ValueError(f"W4A8 q must be a 2D int8 tensor, got {tuple(w.q.shape)} {w.q.dtype}")
+    n, k = w.q.shape[0], w.q.shape[1] * 2
+    gs, cr = w.group_size, w.convrot
+    if gs < 4 or k % 16 or k % gs or k % cr or (16 % gs and gs % 16):
+        raise ValueError(f"K={k} must be divisible by 16, group_size={gs} and convrot={cr}; group_size >= 4 dividing 16 or a multiple of 16")
+    if tuple(w.s_rel.shape) != (n, k // gs):
+        raise ValueError(f"s_rel must have shape {(n, k // gs)}, got {tuple(w.s_rel.shape)}")
+    if tuple(w.s_ch.shape) != (n,):
+        raise ValueError(f"s_ch must have shape {(n,)}, got {tuple(w.s_ch.shape)}")
+    if tuple(w.codebook.shape) != (16,):
+        raise ValueError(f"codebook must have shape (16,), got {tuple(w.codebook.shape)}")
+    return n, k
+
+
+class _DevWeight:
+    """Kernel-ready views of a W4A8Weight: q with contiguous, 8-byte aligned rows, s_rel with contiguous rows,
+    float32 s_ch / codebook.  Copies only what is not already in that form."""
+
+    __slots__ = ("q", "ldq", "s", "lds", "scode", "s_ch", "cb", "n", "k")
+
+    def __init__(self, w: W4A8Weight):
+        self.n, self.k = _check_weight(w)
+        q = w.q.view(torch.int8) if w.q.dtype == torch.uint8 else w.q
+        if q.stride(-1) != 1 or (q.data_ptr() % 8) or (q.shape[0] > 1 and q.stride(0) % 8):
+            q = q.contiguous()
+        self.q, self.ldq = q, (q.stride(0) if q.shape[0] > 1 else q.shape[1])
+        s = w.s_rel
+        self.scode = _lib.scale_code(s.dtype)
+        if s.stride(-1) != 1:
+            s = s.contiguous()
+        self.s, self.lds = s, (s.stride(0) if s.shape[0] > 1 else s.shape[1])
+        self.s_ch = w.s_ch.to(torch.float32).contiguous()
+        self.cb = w.codebook.to(device=q.device, dtype=torch.float32).contiguous()
+
+
+# --------------------------------------------------------------------------------------------- rotation / quantiser
+def rotate(x: torch.Tensor, size: int = CONVROT) -> torch.Tensor:
+    """x[..., K] -> per-`size`-block x @ H in x.dtype, accumulated exactly and rounded once (qlinear.py:118-132)."""
+    if not x.is_floating_point():
+        raise ValueError(f"rotate expects a floating tensor, got {x.dtype}")
+    k = x.shape[-1]
+    if k % size:
+        raise ValueError(f"last dim {k} is not a multiple of the rotation block {size}")
+    hadamard_regular(size)  # validates the size (power of 4)
+    if x.numel() == 0:
+        return x.clone()
+    _need_gpu(x, "rotate")
+    x2 = x.reshape(-1, k)
+    if x.dtype == torch.float64:  # the reference's own fp64 path: one fp64 GEMM
+        y = torch.matmul(x2.reshape(-1, k // size, size), hadamard_regular(size, x.device, x.dtype)).reshape(-1, k)
+        return y.reshape(x.shape)
+    x2 = _rows(x2)
+    y = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    _lib.check(lib.h3k_rotate(x2.data_ptr(), _lib.act_code(x.dtype), x2.shape[0], k, _ld(x2), size, y.data_ptr(),
+                              k, _lib.stream_of(x.device)), "h3k_rotate")
+    return y.reshape(x.shape)
+
+
+@torch.no_grad()
+def _quantize_rows(x2: torch.Tensor, size: int, mode: str) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Rotate + per-row int8 quantisation on the GPU: (int8 [M, K], fp32 [M, 1]) (qlinear.py:267-292)."""
+    m, k = x2.shape
+    q = torch.empty(m, k, dtype=torch.int8, device=x2.device)
+    xs = torch.empty(m, 1, dtype=torch.float32, device=x2.device)
+    if m == 0:
+        return q, xs
+    x2 = _rows(x2)
+    lib = _lib.load()
+    _lib.check(lib.h3k_rotate_quant(x2.data_ptr(), _lib.act_code(x2.dtype), m, k, _ld(x2), size, _lib.MODE[mode],
+                                    q.data_ptr(), k, xs.data_ptr(), _lib.stream_of(x2.device)), "h3k_rotate_quant")
+    return q, xs
+
+
+def quantize_activation(x: torch.Tensor, *, size: int = CONVROT, quant_mode: str = "ck") -> Tuple[torch.Tensor, torch.Tensor]:
+    """x[..., K] -> (int8 [..., K], fp32 scale [..., 1]) of the rotated activation (qlinear.py:295-303)."""
+    _check_mode(quant_mode)
+    k = x.shape[-1]
+    if k % size:
+        raise ValueError(f"last dim {k} is not a multiple of the rotation block {size}")
+    hadamard_regular(size)
+    _need_gpu(x, "quantize_activation")
+    q, s = _quantize_rows(x.reshape(math.prod(x.shape[:-1]), k), size, quant_mode)
+    return q.reshape(x.shape), s.reshape(*x.shape[:-1], 1)
+
+
+# --------------------------------------------------------------------------------------------- weights
+def _decode(dw: _DevWeight, group: int) -> torch.Tensor:
+    w8 = torch.empty(dw.n, dw.k, dtype=torch.int8, device=dw.q.device)
+    if dw.n:
+        lib = _lib.load()
+        _lib.check(lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(), dw.n,
+                                     dw.k, group, w8.data_ptr(), dw.k, _lib.stream_of(dw.q.device)), "h3k_decode_w4")
+    return w8
+
+
+@torch.no_grad()
+def decode_int8_grid(w: W4A8Weight) -> torch.Tensor:
+    """int8 [N, K]: the exact grid the int8 GEMM consumes (qlinear.py:194-204)."""
+    _check_weight(w)
+    _need_gpu(w.q, "decode_int8_grid")
+    return _decode(_DevWeight(w), w.group_size)
+
+
+@torch.no_grad()
+def dequantize(w: W4A8Weight, dtype: torch.dtype = torch.float32, rotated: bool = False, *, rows: Optional[slice] = None) -> torch.Tensor:
+    """Dense [N, K] weight (qlinear.py:207-226): rotated=True the ConvRot basis (grid * s_ch), False the original
+    basis (W_rot @ H per block, fp32, rounded once to dtype).  `rows` restricts to a contiguous row slice."""
+    n, k = _check_weight(w)
+    if rows is not None and rows.step not in (None, 1):
+        raise ValueError("rows must be a contiguous slice")
+    r0, r1, _ = (rows or slice(0, n)).indices(n)
+    _need_gpu(w.q, "dequantize")
+    sub = W4A8Weight(w.q[r0:r1], w.s_rel[r0:r1], w.s_ch[r0:r1], w.codebook, w.group_size, w.convrot)
+    wr = decode_int8_grid(sub).float().mul_(sub.s_ch.float().unsqueeze(1))
+    if not rotated:
+        h = hadamard_regular(w.convrot, w.q.device, torch.float32)
+        wr = torch.matmul(wr.view(max(r1 - r0, 0), k // w.convrot, w.convrot), h).view(max(r1 - r0, 0), k)
+    return wr.to(dtype)
+
+
+# --------------------------------------------------------------------------------------------- backends
+def available_backends() -> Dict[str, Dict[str, Any]]:
+    """{"hip": {...}, "ck": {...}, "torch": {...}} with availability and why a backend is missing."""
+    ok, why = True, None
+    try:
+        _lib.load()
+    except (RuntimeError, OSError) as e:
+        ok, why = False, str(e)
+    gpu = torch.cuda.is_available()
+    return {
+        "hip": {"available": ok and gpu, "library": _lib.LIB_PATH if ok else None,
+                "reason": why if not ok else (None if gpu else "no ROCm device")},
+        "ck": {"available": False, "reason": "comfy_kitchen's CUDA kernels are not part of this build (use 'hip')", "version": None},
+        "torch": {"available": False, "reason": "the portable torch backend is not part of this build (use 'hip')"},
+    }
+
+
+def resolve_backend(x: torch.Tensor, w: Weight, backend: str = "auto", precision: str = "a8") -> str:
+    """The backend `linear` will use: "hip" for a W4A8 weight, "dense" for a dense one (qlinear.py:345-361)."""
+    if backend not in _BACKENDS:
+        raise ValueError(f"backend must be 'auto', 'hip', 'ck' or 'torch', got {backend!r}")
+    if precision not in ("a8", "a16"):
+        raise ValueError(f"precision must be 'a8' or 'a16', got {precision!r}")
+    if not isinstance(w, W4A8Weight):
+        return "dense"
+    if backend in ("ck", "torch"):
+        raise RuntimeError(f"backend {backend!r} unavailable: {available_backends()[backend]['reason']}")
+    return "hip"
+
+
+def _swiglu(x: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up on [gate | up] halves, in x.dtype (qlinear.py:376-379)."""
+    gate, up = x.chunk(2, dim=-1)
+    return F.silu(gate).mul_(up)
+
+
+class _HipRunner:
+    """W4A8 forward for one weight on the GPU: the weight's int8 grid is decoded once per call, then each token
+    chunk runs rotate+quantise and the int8 MFMA GEMM with the fused epilogue into its `out` slice."""
+
+    def __init__(self, w: W4A8Weight, bias: Optional[torch.Tensor], out_dtype: torch.dtype, precision: str, mode: str):
+        self.w, self.out_dtype, self.precision, self.mode = w, out_dtype, precision, mode
+        self.dw = _DevWeight(w)
+        self.n, self.k = self.dw.n, self.dw.k
+        self.ocode = _lib.act_code(out_dtype)
+        self.bias = None if bias is None else bias.to(device=w.q.device, dtype=out_dtype).contiguous()
+        self.w8 = _decode(self.dw, w.group_size)
+        self.lib = _lib.load()
+
+    def __call__(self, x2: torch.Tensor, out: torch.Tensor) -> None:
+        (self._a8 if self.precision == "a8" else self._a16)(x2, out)
+
+    def _a8(self, x2: torch.Tensor, out: torch.Tensor) -> None:
+        m = x2.shape[0]
+        xq, xs = _quantize_rows(x2, self.w.convrot, self.mode)
+        _lib.check(self.lib.h3k_gemm_a8w8(xq.data_ptr(), self.k, xs.data_ptr(), self.w8.data_ptr(), self.k,
+                                          self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
+                                          _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0), None,
+                                          _lib.stream_of(x2.device)), "h3k_gemm_a8w8")
+
+    def _a16(self, x2: torch.Tensor, out: torch.Tensor) -> None:
+        """Unquantised activation (qlinear.py:407-424): rotated x (rounded to x.dtype) times the exact int8 levels
+        with fp32 accumulation, s_ch applied to the fp32 result, rounded once."""
+        xr = rotate(x2, self.w.convrot).to(torch.float32)
+        y = torch.mm(xr, self.w8.to(torch.float32).t())
+        y.mul_(self.dw.s_ch)
+        if self.bias is not None:
+            y.add_(self.bias.to(torch.float32))
+        out.copy_(y)
+
+
+@torch.no_grad()
+def _linear_w4a8(x2, w, bias, out_dtype, backend, precision, swiglu, chunk_tokens, quant_mode):
+    n, k = _check_weight(w)
+    kx = x2.shape[-1] // (2 if swiglu else 1)
+    if kx != k:
+        raise ValueError(f"input features {kx}{' (after swiglu)' if swiglu else ''} do not match the weight's K={k}")
+    if x2.device != w.q.device:
+        raise ValueError(f"input on {x2.device} but weight on {w.q.device}")
+    if bias is not None and tuple(bias.shape) != (n,):
+        raise ValueError(f"bias must have shape {(n,)}, got {tuple(bias.shape)}")
+    m = x2.shape[0]
+    if m == 0:
+        return torch.empty(0, n, dtype=out_dtype, device=x2.device)
+    _need_gpu(x2, "linear")
+    resolve_backend(x2, w, backend, precision)
+    if x2.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"the HIP path takes bf16, f16 or f32 activations, got {x2.dtype}")
+    out = torch.empty(m, n, dtype=out_dtype, device=x2.device)
+    runner = _HipRunner(w, bias, out_dtype, precision, quant_mode)
+    step = min(chunk_tokens or m, m)
+    for a in range(0, m, step):
+        xc = x2[a: a + step]
+        if swiglu:
+            xc = _swiglu(xc)
+        runner(xc, out[a: a + step])
+    return out
+
+
+def linear(
+    x: torch.Tensor,
+    w: Weight,
+    bias: Optional[torch.Tensor] = None,
+    *,
+    out_dtype: Optional[torch.dtype] = None,
+    backend: str = "auto",
+    precision: str = "a8",
+    input_act: Optional[str] = None,
+    chunk_tokens: Optional[int] = None,
+    quant_mode: str = "ck",
+) -> torch.Tensor:
+    """out = act(x) @ W.T + bias over the last dim of x (qlinear.py:466-523).
+
+    w: dense [N, K] tensor (plain F.linear in x.dtype) or W4A8Weight (HIP kernels).
+    precision "a8" quantises activations to int8 per token (the native W4A8 path); "a16" keeps them (rotated x
+    times the exact int8 levels, fp32 accumulation).  input_act="swiglu": x is [gate | up], silu(gate) * up in
+    x.dtype first.  chunk_tokens bounds peak memory; a8 is token-wise, so chunking is bit-exact.
+    """
+    if not x.is_floating_point():
+        raise ValueError(f"x must be floating point, got {x.dtype}")
+    if input_act not in (None, "none", "swiglu"):
+        raise ValueError(f"input_act must be None or 'swiglu', got {input_act!r}")
+    if chunk_tokens is not None and chunk_tokens < 1:
+        raise ValueError("chunk_tokens must be >= 1")
+    _check_mode(quant_mode)
+    swiglu = input_act == "swiglu"
+    if swiglu and x.shape[-1] % 2:
+        raise ValueError(f"swiglu needs an even last dim, got {x.shape[-1]}")
+    out_dtype = out_dtype or x.dtype
+    kind = resolve_backend(x, w, backend, precision)
+    lead = x.shape[:-1]
+    x2 = x.reshape(math.prod(lead), x.shape[-1])
+    if kind != "dense":
+        y = _linear_w4a8(x2, w, bias, out_dtype, backend, precision, swiglu, chunk_tokens, quant_mode)
+        return y.reshape(*lead, y.shape[-1])
+    if x2.shape[-1] // (2 if swiglu else 1) != w.shape[-1]:
+        raise ValueError(f"input features {x2.shape[-1]} do not match the dense weight {tuple(w.shape)}")
+    step = chunk_tokens or max(x2.shape[0], 1)
+    cpu_lowp = x.device.type == "cpu" and x.dtype in (torch.bfloat16, torch.float16)
+    wd = w.to(dtype=torch.float32 if cpu_lowp else x.dtype)
+    bd = None if bias is None else bias.to(dtype=wd.dtype)
+    outs = []
+    for a in range(0, max(x2.shape[0], 1), step):
+        xc = x2[a: a + step]
+        if swiglu:
+            xc = _swiglu(xc)
+        outs.append(F.linear(xc.to(wd.dtype), wd, bd).to(out_dtype))
+    y = outs[0] if len(outs) == 1 else torch.cat(outs, 0)
+    return y.reshape(*lead, y.shape[-1])
+
