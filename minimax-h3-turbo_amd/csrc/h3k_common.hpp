@@ -7,12 +7,25 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 #include "h3k.h"
 
 namespace h3k {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Compile-time loop: f(std::integral_constant<int, i>{}) for i in [0, N).  Register arrays indexed through it
+// only ever see constant indices, so they are promoted to registers before any unrolling happens.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // ------------------------------------------------------------------------------------------ host errors
 void set_error(const char* fmt, ...);
@@ -24,6 +37,14 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 inline bool is_pow4(int r) { return r == 4 || r == 16 || r == 64 || r == 256 || r == 1024; }
 
 // ------------------------------------------------------------------------------------------ number formats
+// Materialise an fp32 value: stops the backend from fusing the operation that produced it with a later
+// narrowing conversion (e.g. fptrunc(fmul) -> v_fma_mixlo_f16 rounds once, where the reference rounds to fp32
+// first and then to f16: the two differ when the fp32 result is an exact f16 tie).
+__device__ __forceinline__ float fp32_round_point(float f) {
+  __asm__ volatile("" : "+v"(f));
+  return f;
+}
+
 // bf16 bits -> float (exact)
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 

@@ -38,13 +38,12 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tn = r / gm;
 }
 
-template <int WMB, int WNB>
+template <int WMB, int WNB, int ODT, bool EAGER>
 __global__ __launch_bounds__(256, 1) void gemm_a8w8_kernel(const int8_t* __restrict__ A, int64_t lda,
                                                            const int8_t* __restrict__ B, int64_t ldb, int M, int N, int K,
                                                            const float* __restrict__ xs, const float* __restrict__ sch,
                                                            const void* __restrict__ bias, void* __restrict__ out,
-                                                           int64_t ldo, int32_t* __restrict__ acc_out, int mode,
-                                                           int out_dtype) {
+                                                           int64_t ldo, int32_t* __restrict__ acc_out) {
   constexpr int BM = 64 * WMB, BN = 64 * WNB;
   constexpr int A_LD = BM / 64, B_LD = BN / 64;  // 16-byte chunks per thread per K step
   __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * kBK];
@@ -89,12 +88,7 @@ __global__ __launch_bounds__(256, 1) void gemm_a8w8_kernel(const int8_t* __restr
   };
 
   v16i acc[WMB][WNB];
-#pragma unroll
-  for (int i = 0; i < WMB; ++i)
-#pragma unroll
-    for (int j = 0; j < WNB; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  static_for<WMB>([&](auto i) { static_for<WNB>([&](auto j) { acc[i][j] = v16i{}; }); });
 
   const int KT = (K + kBK - 1) / kBK;
   gload(0);
@@ -104,19 +98,17 @@ __global__ __launch_bounds__(256, 1) void gemm_a8w8_kernel(const int8_t* __restr
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < KT) gload(kt + 1);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    static_for<2>([&](auto s) {
       v4i af[WMB], bf[WNB];
       const int c = s * 2 + kh;
-#pragma unroll
-      for (int i = 0; i < WMB; ++i) af[i] = *reinterpret_cast<const v4i*>(&sA[cur][swz(arow + i * 32, c)]);
-#pragma unroll
-      for (int j = 0; j < WNB; ++j) bf[j] = *reinterpret_cast<const v4i*>(&sB[cur][swz(brow + j * 32, c)]);
-#pragma unroll
-      for (int i = 0; i < WMB; ++i)
-#pragma unroll
-        for (int j = 0; j < WNB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
+      static_for<WMB>([&](auto i) { af[i] = *reinterpret_cast<const v4i*>(&sA[cur][swz(arow + i * 32, c)]); });
+      static_for<WNB>([&](auto j) { bf[j] = *reinterpret_cast<const v4i*>(&sB[cur][swz(brow + j * 32, c)]); });
+      static_for<WMB>([&](auto i) {
+        static_for<WNB>([&](auto j) {
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        });
+      });
+    });
     if (kt + 1 < KT) lstore(cur ^ 1);
     __syncthreads();
   }
@@ -124,54 +116,63 @@ __global__ __launch_bounds__(256, 1) void gemm_a8w8_kernel(const int8_t* __restr
   // ---------------------------------------------------------------- epilogue
   // C layout of a 32x32 MFMA block: lane l holds column (l % 32); register r holds row
   // (r / 4) * 8 + (l / 32) * 4 + (r % 4).
-  const bool eager = mode == H3K_MODE_EAGER;
-#pragma unroll
-  for (int j = 0; j < WNB; ++j) {
+  static_for<WNB>([&](auto j) {
     const int gn = n0 + wn * (32 * WNB) + j * 32 + (lane & 31);
-    if (gn >= N) continue;
-    const float sc = sch[gn];
+    const bool nok = gn < N;
+    const float sc = nok ? sch[gn] : 0.0f;
     float bv = 0.0f;
-    if (bias) {
-      if (out_dtype == H3K_F32) bv = static_cast<const float*>(bias)[gn];
-      else if (out_dtype == H3K_F16) bv = f16_to_f32(static_cast<const uint16_t*>(bias)[gn]);
+    if (bias && nok) {
+      if (ODT == H3K_F32) bv = static_cast<const float*>(bias)[gn];
+      else if (ODT == H3K_F16) bv = f16_to_f32(static_cast<const uint16_t*>(bias)[gn]);
       else bv = bf16_to_f32(static_cast<const uint16_t*>(bias)[gn]);
     }
-#pragma unroll
-    for (int i = 0; i < WMB; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
+    static_for<WMB>([&](auto i) {
+      static_for<16>([&](auto r) {
         const int gm = m0 + wm * (32 * WMB) + i * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
-        if (gm >= M) continue;
-        const int a = acc[i][j][r];
-        if (acc_out) acc_out[static_cast<int64_t>(gm) * N + gn] = a;
-        const float xv = xs[gm];
-        float f = eager ? static_cast<float>(a) * (xv * sc) : (static_cast<float>(a) * xv) * sc;
-        const int64_t o = static_cast<int64_t>(gm) * ldo + gn;
-        if (out_dtype == H3K_F32) {
-          if (bias) f = f + bv;
-          static_cast<float*>(out)[o] = f;
-        } else if (out_dtype == H3K_F16) {
-          f = round_f16(f);
-          if (bias) f = f + bv;
-          static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_f16_bits(f));
-        } else {
-          f = round_bf16(f);
-          if (bias) f = f + bv;
-          static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_bf16_bits(f));
+        const int a = acc[i][j][decltype(r)::value];
+        if (nok && gm < M) {
+          if (acc_out) acc_out[static_cast<int64_t>(gm) * N + gn] = a;
+          const float xv = xs[gm];
+          float f = fp32_round_point(EAGER ? static_cast<float>(a) * fp32_round_point(xv * sc)
+                                           : fp32_round_point(static_cast<float>(a) * xv) * sc);
+          const int64_t o = static_cast<int64_t>(gm) * ldo + gn;
+          if (ODT == H3K_F32) {
+            if (bias) f = f + bv;
+            static_cast<float*>(out)[o] = f;
+          } else if (ODT == H3K_F16) {
+            f = round_f16(f);
+            if (bias) f = fp32_round_point(f + bv);
+            static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_f16_bits(f));
+          } else {
+            f = round_bf16(f);
+            if (bias) f = fp32_round_point(f + bv);
+            static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_bf16_bits(f));
+          }
         }
-      }
-    }
-  }
+      });
+    });
+  });
+}
+
+template <int WMB, int WNB, int ODT, bool EAGER>
+static void launch_gemm(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k, const float* xs,
+                        const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, hipStream_t st) {
+  constexpr int BM = 64 * WMB, BN = 64 * WNB;
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_a8w8_kernel<WMB, WNB, ODT, EAGER>), dim3(tiles), dim3(256), 0, st, a, lda, b, ldb, m, n, k, xs,
+                     sch, bias, out, ldo, acc);
 }
 
 template <int WMB, int WNB>
-static void launch_gemm(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k, const float* xs,
-                        const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, int mode, int odt,
-                        hipStream_t st) {
-  constexpr int BM = 64 * WMB, BN = 64 * WNB;
-  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_a8w8_kernel<WMB, WNB>), dim3(tiles), dim3(256), 0, st, a, lda, b, ldb, m, n, k, xs, sch, bias,
-                     out, ldo, acc, mode, odt);
+static void launch_gemm_dt(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
+                           const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
+                           int mode, int odt, hipStream_t st) {
+  const bool e = mode == H3K_MODE_EAGER;
+#define H3K_L(D, E) launch_gemm<WMB, WNB, D, E>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st)
+  if (odt == H3K_BF16) { if (e) H3K_L(H3K_BF16, true); else H3K_L(H3K_BF16, false); }
+  else if (odt == H3K_F16) { if (e) H3K_L(H3K_F16, true); else H3K_L(H3K_F16, false); }
+  else { if (e) H3K_L(H3K_F32, true); else H3K_L(H3K_F32, false); }
+#undef H3K_L
 }
 
 int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
@@ -190,9 +191,9 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
     return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
   const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
   if (m >= 2048 && n >= 256)
-    launch_gemm<4, 4>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
+    launch_gemm_dt<4, 4>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
   else
-    launch_gemm<2, 2>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
+    launch_gemm_dt<2, 2>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
   return check_launch("gemm_a8w8");
 }
 

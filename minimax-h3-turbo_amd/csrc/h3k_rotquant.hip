@@ -153,9 +153,9 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
         const float y = to_f32_16<F16>(bits);
         float t;
         if (F16) {
-          t = round_f16(y / s);
+          t = round_f16(fp32_round_point(y / s));
         } else {
-          t = round_bf16(y * rs);
+          t = round_bf16(fp32_round_point(y * rs));
         }
         t = __builtin_rintf(t);
         t = __builtin_amdgcn_fmed3f(t, -128.0f, 127.0f);
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
             static_cast<uint16_t*>(y)[row * ldy + c0 + e] = static_cast<uint16_t>(bits);
           }
         } else {
-          float tq = (DT == H3K_F32) ? (yr / s) : round_dt<DT>(yr / s);
+          float tq = (DT == H3K_F32) ? (yr / s) : round_dt<DT>(fp32_round_point(yr / s));
           tq = __builtin_amdgcn_fmed3f(__builtin_rintf(tq), -128.0f, 127.0f);
           q[row * ldq + c0 + e] = static_cast<int8_t>(static_cast<int>(tq));
         }

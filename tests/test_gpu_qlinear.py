@@ -339,3 +339,50 @@ def test_a8_error_is_the_predicted_quantisation_noise_and_a16_removes_it(wq):
     r16 = ((y16b.double() - want_b).norm() / want_b.norm()).item()
     r8 = ((y8b.double() - want_b).norm() / want_b.norm()).item()
     assert y16b.dtype == torch.bfloat16 and r16 < 0.004 and r16 < 0.5 * r8
+
+
+# ---------------------------------------------------------------------------------------------- epilogue rounding
+def _gemm(xq, xs, w8, s_ch, mode, odt, bias=None):
+    m, k = xq.shape
+    n = w8.shape[0]
+    dt = {_lib.BF16: torch.bfloat16, _lib.F16: torch.float16, _lib.F32: torch.float32}[odt]
+    out = torch.empty(m, n, dtype=dt, device=DEV)
+    acc = torch.empty(m, n, dtype=torch.int32, device=DEV)
+    lib = _lib.load()
+    _lib.check(lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, s_ch.data_ptr(), _lib.ptr(bias), m, n, k,
+                                 _lib.MODE[mode], out.data_ptr(), odt, n, acc.data_ptr(), _lib.stream_of(DEV)), "gemm")
+    return out, acc
+
+
+def test_epilogue_keeps_the_fp32_rounding_before_narrowing():
+    """acc * (xs * s_ch) rounds to fp32 exactly on an f16 tie (23.5078125); the reference then rounds to even
+    (23.5).  A fused multiply-and-narrow would round the exact product once (23.515625)."""
+    a = torch.zeros(1, 16, dtype=torch.int8)
+    w = torch.zeros(1, 16, dtype=torch.int8)
+    a[0, :6] = torch.tensor([127, 127, 127, 127, 127, 5], dtype=torch.int8)
+    w[0, :6] = torch.tensor([127, 127, 127, 127, 60, 10], dtype=torch.int8)
+    xs = torch.tensor([[0.02083846]], dtype=torch.float32)
+    sc = torch.tensor([0.015627649], dtype=torch.float32)
+    out, acc = _gemm(a.to(DEV), xs.to(DEV), w.to(DEV), sc.to(DEV), "eager", _lib.F16)
+    assert acc.item() == 72186
+    assert out.float().item() == 23.5
+    assert out.float().item() == ref.epilogue(np.array([[72186]], np.int32), xs.numpy(), sc.numpy(), "f16", "eager")[0, 0]
+
+
+@pytest.mark.parametrize("mode", ["ck", "eager"])
+@pytest.mark.parametrize("odt", [_lib.BF16, _lib.F16, _lib.F32])
+def test_epilogue_matches_the_oracle_on_random_accumulators(mode, odt):
+    g = torch.Generator().manual_seed(odt * 7 + (mode == "eager"))
+    m, n, k = 512, 520, 1024
+    xq = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8)
+    w8 = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    xs = (torch.rand(m, 1, generator=g) * 0.05 + 1e-4)
+    sc = (torch.rand(n, generator=g) * 0.03 + 1e-4)
+    name = {_lib.BF16: "bf16", _lib.F16: "f16", _lib.F32: "f32"}[odt]
+    dt = {_lib.BF16: torch.bfloat16, _lib.F16: torch.float16, _lib.F32: torch.float32}[odt]
+    bias = torch.randn(n, generator=g).to(dt)
+    out, acc = _gemm(xq.to(DEV), xs.to(DEV), w8.to(DEV), sc.to(DEV), mode, odt, bias.to(DEV))
+    want_acc = ref.int8_mm(xq.numpy(), w8.numpy())
+    assert np.array_equal(acc.cpu().numpy(), want_acc)
+    want = ref.epilogue(want_acc, xs.numpy(), sc.numpy(), name, mode, bias.float().numpy())
+    assert np.array_equal(out.float().cpu().numpy(), want)
