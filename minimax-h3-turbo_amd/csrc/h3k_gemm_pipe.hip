@@ -1,0 +1,292 @@
+// Large-shape int8 x int8 -> int32 GEMM for gfx950 with the W4A8 epilogue fused: the deep-pipeline variant.
+//
+// Same contract as gemm_a8w8_kernel (h3k_gemm.hip):
+//   acc[m, n] = sum_k a[m, k] * w8[n, k]                         exact int32
+//   ck   : out = round(f32(f32(acc) * xs[m]) * s_ch[n])          reference h3turbo/h3/qlinear.py:401
+//   eager: out = round(f32(acc) * f32(xs[m] * s_ch[n]))          reference h3turbo/h3/qlinear.py:403
+//   bias : out = round(f32(out) + f32(bias[n]))                  reference h3turbo/h3/qlinear.py:404-405
+// for K a multiple of 64.
+//
+// Data movement: global -> LDS with the gfx950 direct-to-LDS load (global_load_lds_dwordx4: each lane's 16
+// bytes land at M0 + 16 * lane, no register staging), into a ring of S stages of BK = 64 bytes of K.  Stage
+// kt + S is issued as soon as every wave has finished reading stage kt, so S - 1 stages of loads are in flight
+// while one is multiplied: the HBM/L2 latency is hidden behind (S - 1) x BM x BN x 64 MACs of MFMA work.
+// Waits are explicit (s_waitcnt vmcnt / lgkmcnt, then s_barrier) instead of __syncthreads, whose release fence
+// would drain every outstanding load, prefetches included.
+//
+// LDS layout of a stage: A rows [BM][64 B] then B rows [BN][64 B].  The four 16-byte chunks of a row are
+// XOR-swizzled by (row >> 1) & 3, so the 16-byte MFMA fragment reads (32 rows x one chunk per half-wave) are
+// bank-conflict free.  A direct-to-LDS load writes 1 KiB contiguously (16 rows); the swizzle is applied on the
+// global side instead, by choosing which chunk each lane fetches.  Rows past M or N are clamped to the last
+// valid row (their products only reach output rows/columns that are never stored).
+//
+// MFMA: v_mfma_i32_32x32x32_i8.  The workgroup (WM x WN wavefronts) owns a BM x BN output tile; a wavefront
+// owns (BM / WM) x (BN / WN) as WMB x WNB blocks of 32 x 32 held in accumulation registers.  Within a K-step
+// the two 32-byte halves are software-pipelined: fragments of half 1 are read while half 0 multiplies, and
+// the fragments of the next K-step's half 0 while half 1 multiplies.
+#include "h3k_common.hpp"
+
+namespace h3k {
+
+namespace pipe {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kBK = 64;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt [11:8])
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// Workgroup barrier that orders LDS accesses (and the direct-to-LDS loads the caller has waited for) without
+// the memory-model fence of __syncthreads.  The empty asm statements keep the compiler from moving memory
+// operations across it; sched_barrier keeps the machine scheduler from doing so.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ int swz(int r, int c) { return r * kBK + ((c ^ ((r >> 1) & 3)) << 4); }
+
+// tile id -> (tile_m, tile_n): XCD-contiguous ranges, then groups of GM tile-rows walked column by column
+template <int GM>
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int per = total >> 3, rem = total & 7;
+  const int id = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int in_group = GM * tiles_n;
+  const int gid = id / in_group;
+  const int first_m = gid * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int r = id - gid * in_group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
+
+template <int WM, int WN, int WMB, int WNB, int S, int MINB, int ODT, bool EAGER>
+__global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int8_t* __restrict__ A, int64_t lda,
+                                                                    const int8_t* __restrict__ B, int64_t ldb, int M,
+                                                                    int N, int K, const float* __restrict__ xs,
+                                                                    const float* __restrict__ sch,
+                                                                    const void* __restrict__ bias,
+                                                                    void* __restrict__ out, int64_t ldo,
+                                                                    int32_t* __restrict__ acc_out, bool vec_out,
+                                                                    bool vec_acc) {
+  constexpr int NW = WM * WN;
+  constexpr int BM = 32 * WMB * WM, BN = 32 * WNB * WN;
+  constexpr int STAGE = (BM + BN) * kBK;           // bytes per stage
+  constexpr int D = STAGE / 1024;                  // 1 KiB direct-to-LDS loads per stage
+  constexpr int DPW = D / NW;                      // ... per wavefront
+  static_assert(D % NW == 0, "stage loads must split evenly over the wavefronts");
+  static_assert(BM % 16 == 0 && BN % 16 == 0, "16-row load granules");
+  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE];
+
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords<8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  // per-lane global source of each of this wave's DPW loads (K offset added per stage)
+  const int8_t* src[DPW];
+  static_for<DPW>([&](auto i) {
+    const int d = wave * DPW + i;  // load granule within the stage
+    const int lr = (lane >> 2);
+    if (d < BM / 16) {
+      const int r = d * 16 + lr;
+      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      const int gr = min(m0 + r, M - 1);
+      src[i] = A + static_cast<int64_t>(gr) * lda + c * 16;
+    } else {
+      const int r = (d - BM / 16) * 16 + lr;
+      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      const int gr = min(n0 + r, N - 1);
+      src[i] = B + static_cast<int64_t>(gr) * ldb + c * 16;
+    }
+  });
+  auto issue = [&](int kt, int buf) {
+    static_for<DPW>([&](auto i) {
+      int8_t* dst = smem + buf * STAGE + (wave * DPW + i) * 1024;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src[i] + static_cast<int64_t>(kt) * kBK),
+                                       (lds_void*)(dst), 16, 0, 0);
+    });
+  };
+
+  const int arow = wm * (32 * WMB) + (lane & 31), brow = BM + wn * (32 * WNB) + (lane & 31), kh = lane >> 5;
+  auto read_frags = [&](int buf, int half, v4i (&af)[WMB], v4i (&bf)[WNB]) {
+    const int8_t* base = smem + buf * STAGE;
+    const int c = half * 2 + kh;
+    static_for<WMB>([&](auto i) { af[i] = *reinterpret_cast<const v4i*>(base + swz(arow + i * 32, c)); });
+    static_for<WNB>([&](auto j) { bf[j] = *reinterpret_cast<const v4i*>(base + swz(brow + j * 32, c)); });
+  };
+
+  v16i acc[WMB][WNB];
+  static_for<WMB>([&](auto i) { static_for<WNB>([&](auto j) { acc[i][j] = v16i{}; }); });
+  auto mfma = [&](const v4i (&af)[WMB], const v4i (&bf)[WNB]) {
+    static_for<WMB>([&](auto i) {
+      static_for<WNB>([&](auto j) {
+        // operands swapped (B A^T): the accumulator layout then gives each lane one output row (see epilogue)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+      });
+    });
+  };
+
+  const int KT = K / kBK;
+  // prologue: fill the ring, wait for stage 0
+  static_for<S>([&](auto s) {
+    if (s < KT) issue(s, s);
+  });
+  if (KT >= S) wait_vmcnt<DPW * (S - 1)>();
+  else wait_vmcnt<0>();
+  lds_barrier();
+
+  v4i a0[WMB], b0[WNB], a1[WMB], b1[WNB];
+  read_frags(0, 0, a0, b0);
+  int buf = 0;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int nbuf = buf + 1 == S ? 0 : buf + 1;
+    read_frags(buf, 1, a1, b1);
+    mfma(a0, b0);
+    // every read of this stage has landed; the next stage's loads (issued S-1 steps ago) have too
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkmcnt0();
+    if (kt + S <= KT) wait_vmcnt<DPW * (S - 2)>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (kt + S < KT) issue(kt + S, buf);
+    if (kt + 1 < KT) read_frags(nbuf, 0, a0, b0);
+    mfma(a1, b1);
+    buf = nbuf;
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  // With the operands swapped, block (i, j) holds C^T: lane l owns output row m = i * 32 + (l % 32) and
+  // register r the column n = j * 32 + (r / 4) * 8 + (l / 32) * 4 + (r % 4), i.e. four consecutive columns per
+  // r / 4, stored with one 8-byte (16-bit outputs) or 16-byte (fp32 / int32) store.  Scales are loaded once.
+  const int mrow = m0 + wm * (32 * WMB) + (lane & 31);
+  const int ncol = n0 + wn * (32 * WNB) + kh * 4;
+  float xv[WMB];
+  static_for<WMB>([&](auto i) {
+    const int m = mrow + i * 32;
+    xv[i] = m < M ? xs[m] : 0.0f;
+  });
+  auto value = [&](int a, float x, float s, float b) -> float {
+    float f = fp32_round_point(EAGER ? static_cast<float>(a) * fp32_round_point(x * s)
+                                     : fp32_round_point(static_cast<float>(a) * x) * s);
+    if (ODT == H3K_F32) return bias ? f + b : f;
+    f = ODT == H3K_F16 ? round_f16(f) : round_bf16(f);
+    return bias ? fp32_round_point(f + b) : f;
+  };
+  auto bits16 = [&](float f) -> uint32_t { return ODT == H3K_F16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f); };
+  static_for<WNB>([&](auto j) {
+    float sc[16], bv[16];
+    static_for<16>([&](auto r) {
+      const int n = ncol + j * 32 + (r >> 2) * 8 + (r & 3);
+      sc[r] = n < N ? sch[n] : 0.0f;
+      float b = 0.0f;
+      if (bias && n < N) {
+        if (ODT == H3K_F32) b = static_cast<const float*>(bias)[n];
+        else if (ODT == H3K_F16) b = f16_to_f32(static_cast<const uint16_t*>(bias)[n]);
+        else b = bf16_to_f32(static_cast<const uint16_t*>(bias)[n]);
+      }
+      bv[r] = b;
+    });
+    static_for<WMB>([&](auto i) {
+      const int m = mrow + i * 32;
+      if (m < M) {
+        static_for<4>([&](auto g) {
+          const int n = ncol + j * 32 + g * 8;
+          int a[4];
+          float f[4];
+          static_for<4>([&](auto e) {
+            a[e] = acc[i][j][g * 4 + e];
+            f[e] = value(a[e], xv[i], sc[g * 4 + e], bv[g * 4 + e]);
+          });
+          const int64_t o = static_cast<int64_t>(m) * ldo + n;
+          if (n + 3 < N && vec_out) {
+            if (ODT == H3K_F32) {
+              *reinterpret_cast<float4*>(static_cast<float*>(out) + o) = make_float4(f[0], f[1], f[2], f[3]);
+            } else {
+              *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + o) =
+                  make_uint2(bits16(f[0]) | (bits16(f[1]) << 16), bits16(f[2]) | (bits16(f[3]) << 16));
+            }
+          } else {
+            static_for<4>([&](auto e) {
+              if (n + e < N) {
+                if (ODT == H3K_F32) static_cast<float*>(out)[o + e] = f[e];
+                else static_cast<uint16_t*>(out)[o + e] = static_cast<uint16_t>(bits16(f[e]));
+              }
+            });
+          }
+          if (acc_out) {
+            const int64_t oa = static_cast<int64_t>(m) * N + n;
+            if (n + 3 < N && vec_acc) {
+              *reinterpret_cast<int4*>(acc_out + oa) = make_int4(a[0], a[1], a[2], a[3]);
+            } else {
+              static_for<4>([&](auto e) {
+                if (n + e < N) acc_out[oa + e] = a[e];
+              });
+            }
+          }
+        });
+      }
+    });
+  });
+}
+
+#ifndef H3K_PIPE_CFG
+#define H3K_PIPE_CFG 0
+#endif
+
+// tile configurations: (WM, WN, WMB, WNB, S, workgroups per CU)
+#if H3K_PIPE_CFG == 0
+constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 4, cMINB = 1;  // 256 x 256, 8 waves
+#elif H3K_PIPE_CFG == 1
+constexpr int cWM = 2, cWN = 2, cWMB = 4, cWNB = 4, cS = 4, cMINB = 1;  // 256 x 256, 4 waves
+#elif H3K_PIPE_CFG == 2
+constexpr int cWM = 2, cWN = 2, cWMB = 4, cWNB = 2, cS = 3, cMINB = 2;  // 256 x 128, 4 waves, 2 workgroups per CU
+#elif H3K_PIPE_CFG == 3
+constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 2, cMINB = 1;  // 256 x 256, 8 waves, 2 stages
+#endif
+
+template <int ODT, bool EAGER>
+static void launch_pipe(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
+                        const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
+                        hipStream_t st) {
+  constexpr int BM = 32 * cWMB * cWM, BN = 32 * cWNB * cWN;
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  // vector stores of 4 consecutive outputs need their address aligned to 4 elements
+  const size_t es = ODT == H3K_F32 ? 4 : 2;
+  const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
+  const bool vec_acc = acc == nullptr || (aligned(acc, 16) && n % 4 == 0);
+  hipLaunchKernelGGL((gemm_pipe_kernel<cWM, cWN, cWMB, cWNB, cS, cMINB, ODT, EAGER>), dim3(tiles), dim3(cWM * cWN * 64), 0,
+                     st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
+}
+
+}  // namespace pipe
+
+// K % 64 == 0, operands 16-byte aligned with 16-byte multiple strides (checked by the caller)
+void gemm_pipe_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
+                      const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo,
+                      int32_t* acc_out, hipStream_t st) {
+  const bool e = mode == H3K_MODE_EAGER;
+#define H3K_L(D, E) pipe::launch_pipe<D, E>(a, lda, w8, ldw, m, n, k, xs, s_ch, bias, out, ldo, acc_out, st)
+  if (odt == H3K_BF16) { if (e) H3K_L(H3K_BF16, true); else H3K_L(H3K_BF16, false); }
+  else if (odt == H3K_F16) { if (e) H3K_L(H3K_F16, true); else H3K_L(H3K_F16, false); }
+  else { if (e) H3K_L(H3K_F32, true); else H3K_L(H3K_F32, false); }
+#undef H3K_L
+}
+
+}  // namespace h3k
