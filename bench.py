@@ -39,17 +39,51 @@ def parse():
     ap.add_argument("--n", type=int, default=13824)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="after the timed region, run 3 plain device-to-device copies of BYTES bytes: the reference "
+                         "kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic figures")
     return ap.parse_args()
 
 
-def traffic_from_profiles(kernel: str):
-    """HBM bytes per launch measured by rocprofv3 PMC runs and committed under profiles/ (None if absent)."""
+def traffic_from_profiles(key: str):
+    """HBM bytes per launch of `key` ("<kernel> m=.. k=.. n=.."), from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    summarised under profiles/ (None when that workload was not profiled)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(kernel)
+            return json.load(f).get(key)
     except (OSError, ValueError):
         return None
+
+
+def synth_weight(n: int, k: int, dev, seed: int = 0, group: int = 128, convrot: int = 256):
+    """BASELINE weight recipe on the device: W ~ N(0, 0.02) [n, k] rotated into the ConvRot basis, symmetric int4
+    per group of 128 with fp16 relative scales: s_g = amax|W_rot| / 7, code = clamp(rint(W_rot / s_g), -8, 7) + 8
+    (low nibble = even k), codebook arange(-8, 8), s_ch = max_g s_g / 15.875, s_rel = fp16(s_g / s_ch)."""
+    import torch
+
+    from h3turbo_amd import qlinear as ql
+
+    g = torch.Generator(device=dev).manual_seed(seed + 1000)
+    w = torch.randn(n, k, generator=g, device=dev) * 0.02
+    h = ql.hadamard_regular(convrot, dev, torch.float32)
+    w_rot = torch.mm(w.view(-1, convrot), h).view(n, k // group, group)
+    del w
+    s_g = (w_rot.abs().amax(-1) / 7.0).clamp_min(1e-12)
+    code = torch.clamp(torch.round(w_rot / s_g[..., None]), -8, 7).to(torch.int16).view(n, k) + 8
+    del w_rot
+    q = (code[:, 0::2] | (code[:, 1::2] << 4)).to(torch.uint8).view(torch.int8).contiguous()
+    s_ch = (s_g.amax(1) / 15.875).contiguous()
+    s_rel = (s_g / s_ch[:, None]).to(torch.float16).contiguous()
+    cb = torch.arange(-8, 8, dtype=torch.float32, device=dev)
+    return q, s_rel, s_ch, cb
+
+
+def gemm_kernel_name(m: int, n: int, k: int) -> str:
+    """The GEMM kernel h3k_gemm_a8w8 dispatches for this shape (the rule of gemm_a8w8_launch in h3k_gemm.hip)."""
+    if k % 64 == 0 and m > 512 and n >= 256:
+        return "gemm_pipe_kernel"
+    return "gemm_a8w8_kernel"
 
 
 def cpu_baseline(m: int, k: int, n: int, rows: int):
@@ -107,10 +141,7 @@ def main() -> None:
     idx = torch.randperm(k, generator=g, device=dev)[: round(0.01 * k)]
     x[:, idx] *= 20
     x = x.to(torch.bfloat16)
-    q = torch.randint(-128, 128, (n, k // 2), generator=g, dtype=torch.int8, device=dev)
-    s_rel = (torch.rand(n, k // 128, generator=g, device=dev) * 15.0 + 0.875).to(torch.float16)
-    s_ch = torch.rand(n, generator=g, device=dev) * 1e-3 + 1e-4
-    cb = torch.arange(-8, 8, dtype=torch.float32, device=dev)
+    q, s_rel, s_ch, cb = synth_weight(n, k, dev)
     w = W4A8Weight(q, s_rel, s_ch, cb, group_size=128, convrot=256)
 
     lib = _lib.load()
@@ -186,8 +217,8 @@ def main() -> None:
                    "m": m, "k": k, "n": n, "group": 128, "convrot": 256},
         "pct_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles("gemm_a8w8"),
-                     "kernel": "gemm_a8w8_kernel", "kernel_ms": round(t_gemm, 4)},
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(f"{gemm_kernel_name(m, n, k)} m={m} k={k} n={n}"),
+                     "kernel": gemm_kernel_name(m, n, k), "kernel_ms": round(t_gemm, 4)},
         "kernels": {
             "rotate_quant": {"ms": round(t_rq, 4), "GB/s": round(rq_bytes / (t_rq * 1e-3) / 1e9, 1),
                              "frac_hbm": round(rq_bytes / (t_rq * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
@@ -196,6 +227,14 @@ def main() -> None:
             "gemm_a8w8": {"ms": round(t_gemm, 4), "TOPS": round(gemm_tops, 1)},
         },
     }
+    if args.copy_probe:
+        src = torch.full((args.copy_probe,), 1, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            torch.bitwise_not(src, out=dst)  # one plain read + write pass over copy_probe bytes
+        torch.cuda.synchronize()
+        line["copy_probe_bytes"] = args.copy_probe
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(m, k, n, args.cpu_rows)
     print(json.dumps(line), flush=True)

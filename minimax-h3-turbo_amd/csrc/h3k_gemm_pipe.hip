@@ -55,7 +55,21 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-__device__ __forceinline__ int swz(int r, int c) { return r * kBK + ((c ^ ((r >> 1) & 3)) << 4); }
+#ifndef H3K_PIPE_SWZ
+#define H3K_PIPE_SWZ 1
+#endif
+#ifndef H3K_PIPE_GM
+#define H3K_PIPE_GM 8
+#endif
+// physical 16-byte chunk of logical chunk c in LDS row r
+__device__ __forceinline__ int swz_chunk(int r, int c) {
+#if H3K_PIPE_SWZ == 0
+  return c ^ ((r >> 1) & 3);
+#else
+  return c ^ (((r >> 1) ^ (r >> 3)) & 3);
+#endif
+}
+__device__ __forceinline__ int swz(int r, int c) { return r * kBK + (swz_chunk(r, c) << 4); }
 
 // tile id -> (tile_m, tile_n): XCD-contiguous ranges, then groups of GM tile-rows walked column by column
 template <int GM>
@@ -73,7 +87,7 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tn = r / gm;
 }
 
-template <int WM, int WN, int WMB, int WNB, int S, int MINB, int ODT, bool EAGER>
+template <int WM, int WN, int WMB, int WNB, int S, int U, int MINB, int ODT, bool EAGER>
 __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int8_t* __restrict__ A, int64_t lda,
                                                                     const int8_t* __restrict__ B, int64_t ldb, int M,
                                                                     int N, int K, const float* __restrict__ xs,
@@ -89,11 +103,12 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
   constexpr int DPW = D / NW;                      // ... per wavefront
   static_assert(D % NW == 0, "stage loads must split evenly over the wavefronts");
   static_assert(BM % 16 == 0 && BN % 16 == 0, "16-row load granules");
+  static_assert(U >= 1 && S >= 2 * U, "a group of U stages is read while the next U land");
   __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE];
 
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_coords<8>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_coords<H3K_PIPE_GM>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -106,12 +121,12 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
     const int lr = (lane >> 2);
     if (d < BM / 16) {
       const int r = d * 16 + lr;
-      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      const int c = swz_chunk(r, lane & 3);
       const int gr = min(m0 + r, M - 1);
       src[i] = A + static_cast<int64_t>(gr) * lda + c * 16;
     } else {
       const int r = (d - BM / 16) * 16 + lr;
-      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      const int c = swz_chunk(BM + r, lane & 3);
       const int gr = min(n0 + r, N - 1);
       src[i] = B + static_cast<int64_t>(gr) * ldb + c * 16;
     }
@@ -144,31 +159,46 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
   };
 
   const int KT = K / kBK;
-  // prologue: fill the ring, wait for stage 0
+  auto ring = [](int b) { return b >= S ? b - S : b; };
+  // prologue: fill the ring, wait for the first U stages
   static_for<S>([&](auto s) {
     if (s < KT) issue(s, s);
   });
-  if (KT >= S) wait_vmcnt<DPW * (S - 1)>();
+  int issued = KT < S ? KT : S;
+  if (KT >= S) wait_vmcnt<DPW * (S - U)>();
   else wait_vmcnt<0>();
   lds_barrier();
 
+  // Groups of U K-steps between barriers.  At the barrier closing group kt the next group's stages must have
+  // landed; stages issued after them (at most S - 2U) may still be in flight.  The U buffers just read are then
+  // refilled with the stages U groups ahead.
   v4i a0[WMB], b0[WNB], a1[WMB], b1[WNB];
   read_frags(0, 0, a0, b0);
-  int buf = 0;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int nbuf = buf + 1 == S ? 0 : buf + 1;
-    read_frags(buf, 1, a1, b1);
-    mfma(a0, b0);
-    // every read of this stage has landed; the next stage's loads (issued S-1 steps ago) have too
-    __builtin_amdgcn_sched_barrier(0);
-    wait_lgkmcnt0();
-    if (kt + S <= KT) wait_vmcnt<DPW * (S - 2)>();
-    else wait_vmcnt<0>();
-    lds_barrier();
-    if (kt + S < KT) issue(kt + S, buf);
-    if (kt + 1 < KT) read_frags(nbuf, 0, a0, b0);
-    mfma(a1, b1);
-    buf = nbuf;
+  int buf = 0;  // ring buffer of step kt
+  for (int kt = 0; kt < KT; kt += U) {
+    static_for<U>([&](auto u) {
+      read_frags(ring(buf + u), 1, a1, b1);
+      mfma(a0, b0);
+      if (u + 1 < U) {
+        read_frags(ring(buf + u + 1), 0, a0, b0);
+        mfma(a1, b1);
+      } else {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        if (issued == kt + S && kt + S <= KT) wait_vmcnt<DPW * (S - 2 * U)>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        static_for<U>([&](auto v) {
+          if (issued < KT) {
+            issue(issued, ring(buf + v));
+            ++issued;
+          }
+        });
+        if (kt + U < KT) read_frags(ring(buf + U), 0, a0, b0);
+        mfma(a1, b1);
+      }
+    });
+    buf = ring(buf + U);
   }
 
   // ---------------------------------------------------------------- epilogue
@@ -250,15 +280,15 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
 #define H3K_PIPE_CFG 0
 #endif
 
-// tile configurations: (WM, WN, WMB, WNB, S, workgroups per CU)
+// tile configurations: (WM, WN, WMB, WNB, S stages, U stages per barrier, workgroups per CU)
 #if H3K_PIPE_CFG == 0
-constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 4, cMINB = 1;  // 256 x 256, 8 waves
+constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 4, cU = 1, cMINB = 1;  // 256 x 256, 8 waves
 #elif H3K_PIPE_CFG == 1
-constexpr int cWM = 2, cWN = 2, cWMB = 4, cWNB = 4, cS = 4, cMINB = 1;  // 256 x 256, 4 waves
+constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 5, cU = 2, cMINB = 1;  // 256 x 256, 8 waves, 160 KiB
 #elif H3K_PIPE_CFG == 2
-constexpr int cWM = 2, cWN = 2, cWMB = 4, cWNB = 2, cS = 3, cMINB = 2;  // 256 x 128, 4 waves, 2 workgroups per CU
+constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 4, cU = 2, cMINB = 1;  // 256 x 256, 8 waves
 #elif H3K_PIPE_CFG == 3
-constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 2, cMINB = 1;  // 256 x 256, 8 waves, 2 stages
+constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 5, cU = 1, cMINB = 1;  // 256 x 256, 8 waves, 160 KiB
 #endif
 
 template <int ODT, bool EAGER>
@@ -271,8 +301,12 @@ static void launch_pipe(const int8_t* a, int64_t lda, const int8_t* b, int64_t l
   const size_t es = ODT == H3K_F32 ? 4 : 2;
   const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
   const bool vec_acc = acc == nullptr || (aligned(acc, 16) && n % 4 == 0);
-  hipLaunchKernelGGL((gemm_pipe_kernel<cWM, cWN, cWMB, cWNB, cS, cMINB, ODT, EAGER>), dim3(tiles), dim3(cWM * cWN * 64), 0,
-                     st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
+  if ((k / kBK) % cU == 0)
+    hipLaunchKernelGGL((gemm_pipe_kernel<cWM, cWN, cWMB, cWNB, cS, cU, cMINB, ODT, EAGER>), dim3(tiles),
+                       dim3(cWM * cWN * 64), 0, st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
+  else  // K-step count not a multiple of the group: one stage per barrier
+    hipLaunchKernelGGL((gemm_pipe_kernel<cWM, cWN, cWMB, cWNB, 4, 1, cMINB, ODT, EAGER>), dim3(tiles),
+                       dim3(cWM * cWN * 64), 0, st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
 }
 
 }  // namespace pipe
