@@ -90,3 +90,39 @@ def weight_fp8_g16(n: int, k: int, seed: int = 0, group: int = 16, codebook=None
 def bias(n: int, seed: int = 0) -> np.ndarray:
     g = torch.Generator().manual_seed(seed + 77)
     return torch.randn(n, generator=g).numpy().astype(np.float32)
+
+
+# --------------------------------------------------------------------------------------------- DiT block inputs
+def block_case(hidden: int, heads: int, head_dim: int, ffn: int, act: str, s: int, seed: int = 0, rope_freqs: int = 16,
+               fmt: str = "g128"):
+    """Synthetic inputs of one DiT block, all CPU torch / numpy:
+    x bf16 [s, hidden] ~N(0,1); six modulation tensors fp32 [3, hidden] ~N(0, 0.1); segments (token ranges on rows
+    0, 1 and a per-token row tensor); rotary cos/sin bf16 [s, 3F] from random integer (t, h, w) positions;
+    norm weights ~1 + N(0, 0.1); four W4A8 linears (qkv [3*inner, hidden], out [hidden, inner],
+    fc1 [ffn or 2*ffn, hidden], fc2 [hidden, ffn]) in the BASELINE int4 group-128 recipe (fmt "g128") or the
+    reference tests' fp8 group-16 recipe (fmt "fp8")."""
+    g = torch.Generator().manual_seed(seed)
+    inner = heads * head_dim
+    x = torch.randn(s, hidden, generator=g).to(torch.bfloat16)
+    mods = [torch.randn(3, hidden, generator=g) * 0.1 for _ in range(6)]
+    cut1, cut2 = s // 3, (2 * s) // 3
+    per_token = torch.randint(0, 3, (s - cut2,), generator=g)
+    segments = [(0, cut1, 0), (cut1, cut2, 1), (cut2, s, per_token)]
+    pos = torch.randint(0, 64, (s, 3), generator=g)
+    inv_freq = 1.0 / (10000.0 ** (torch.arange(rope_freqs, dtype=torch.float32) / rope_freqs))
+    ang = (pos.float()[:, :, None] * inv_freq[None, None, :]).reshape(s, -1)
+    cos, sin = torch.cos(ang).to(torch.bfloat16), torch.sin(ang).to(torch.bfloat16)
+    norms = {n: (1.0 + 0.1 * torch.randn(d, generator=g)) for n, d in
+             (("norm1", hidden), ("norm2", hidden), ("q_norm", head_dim), ("k_norm", head_dim))}
+    fc1_out = 2 * ffn if act == "swiglu" else ffn
+    lin = {}
+    for i, (name, n, k) in enumerate((("qkv", 3 * inner, hidden), ("out", hidden, inner), ("fc1", fc1_out, hidden),
+                                      ("fc2", hidden, ffn))):
+        if fmt == "g128":
+            q, s_rel, s_ch, cb = weight_int4_g128(n, k, seed=seed * 10 + i)
+            lin[name] = {"q": q, "s_rel": s_rel, "s_kind": "f16", "s_ch": s_ch, "cb": cb, "group": 128, "convrot": 256}
+        else:
+            q, s_rel, s_ch, cb = weight_fp8_g16(n, k, seed=seed * 10 + i)
+            lin[name] = {"q": q, "s_rel": s_rel, "s_kind": "fp8", "s_ch": (s_ch * 0.05).astype(np.float32), "cb": cb,
+                         "group": 16, "convrot": 256}
+    return x, mods, segments, (cos, sin), norms, lin
