@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--k", type=int, default=5120)
     ap.add_argument("--n", type=int, default=13824)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-block", action="store_true", help="skip the config-4 DiT block measurement")
+    ap.add_argument("--block-steps", type=int, default=5)
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="after the timed region, run 3 plain device-to-device copies of BYTES bytes: the reference "
@@ -84,6 +86,71 @@ def gemm_kernel_name(m: int, n: int, k: int) -> str:
     if k % 64 == 0 and m > 512 and n >= 256:
         return "gemm_pipe_kernel"
     return "gemm_a8w8_kernel"
+
+
+def block_measurement(dev, steps: int, warmup: int):
+    """one H3-shape DiT block on the GPU (hidden 5120, 40 x 128 heads, GELU FFN 13824,
+    S = 12090 video + 512 text tokens, bf16, AdaLN modulation precomputed ~N(0, 0.1), all four large linears
+    W4A8 ConvRot QLinear with random-init weights of the BASELINE recipe, attention on PyTorch-ROCm SDPA).
+    Returns the block's mean time over `steps` plus a split measured by running the same linears and SDPA alone."""
+    import torch
+
+    from h3turbo_amd import block as bk
+    from h3turbo_amd import qlinear as ql
+    from h3turbo_amd.types import BlockWeights, W4A8Weight
+
+    s, hidden, heads, hd, ffn = 12602, 5120, 40, 128, 13824
+    cfg = bk.BlockConfig(hidden=hidden, heads=heads, head_dim=hd, ffn=ffn, act="gelu")
+    g = torch.Generator(device=dev).manual_seed(1)
+
+    def lin(n, k, seed):
+        q, s_rel, s_ch, cb = synth_weight(n, k, dev, seed=seed)
+        return W4A8Weight(q, s_rel, s_ch, cb, group_size=128, convrot=256)
+
+    ones = lambda d: 1.0 + 0.1 * torch.randn(d, generator=g, device=dev)  # noqa: E731
+    w = BlockWeights(qkv=lin(3 * cfg.inner, hidden, 11), out=lin(hidden, cfg.inner, 12), fc1=lin(ffn, hidden, 13),
+                     fc2=lin(hidden, ffn, 14), norm1=ones(hidden), norm2=ones(hidden), q_norm=ones(hd), k_norm=ones(hd))
+    x0 = torch.randn(s, hidden, generator=g, device=dev).to(torch.bfloat16)
+    mods = [torch.randn(1, hidden, generator=g, device=dev) * 0.1 for _ in range(6)]
+    segs = [(0, s, 0)]
+    pos = torch.stack(torch.meshgrid(torch.arange(31), torch.arange(15), torch.arange(26), indexing="ij"), -1).reshape(-1, 3)
+    pos = torch.cat([pos + 1, torch.zeros(512, 3, dtype=pos.dtype)], 0)
+    rope = bk.rope_tables(pos, 1.0 / (10000.0 ** (torch.arange(16) / 16.0)), dev, torch.bfloat16)
+    blk = bk.DiTBlock(cfg)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, n):
+        evs = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in evs) / n
+
+    xs = [x0.clone() for _ in range(warmup + steps)]
+    it = iter(xs)
+    timed(lambda: blk(next(it), w, mods, segs, rope), warmup)
+    t_block = timed(lambda: blk(next(it), w, mods, segs, rope), steps)
+    # split: the same calls alone, on inputs of the block's shapes
+    h = torch.randn(s, hidden, generator=g, device=dev).to(torch.bfloat16)
+    o = torch.randn(s, cfg.inner, generator=g, device=dev).to(torch.bfloat16)
+    z = torch.randn(s, ffn, generator=g, device=dev).to(torch.bfloat16)
+    t_lin = {name: timed(fn, steps) for name, fn in (("qkv", lambda: ql.linear(h, w.qkv)), ("out", lambda: ql.linear(o, w.out)),
+                                                     ("fc1", lambda: ql.linear(h, w.fc1)), ("fc2", lambda: ql.linear(z, w.fc2)))}
+    qh, kh, vh = (torch.randn(1, heads, s, hd, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    t_sdpa = timed(lambda: bk._sdpa(qh, kh, vh), steps)
+    lin_ms = sum(t_lin.values())
+    ops = 2.0 * s * hidden * (3 * cfg.inner + cfg.inner + 2 * ffn)
+    sdpa_flop = 4.0 * s * s * hd * heads
+    return {"config": "hidden 5120, 40x128 heads, GELU FFN 13824, S=12090+512, bf16, W4A8 linears, SDPA",
+            "ms": round(t_block, 3), "steps": steps,
+            "split_standalone_ms": {"linears": round(lin_ms, 3), **{k: round(v, 3) for k, v in t_lin.items()},
+                                    "sdpa": round(t_sdpa, 3), "rest": round(t_block - lin_ms - t_sdpa, 3)},
+            "linears_int8_TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1),
+            "sdpa_bf16_TFLOPS": round(sdpa_flop / (t_sdpa * 1e-3) / 1e12, 1)}
 
 
 def cpu_baseline(m: int, k: int, n: int, rows: int):
@@ -227,6 +294,9 @@ def main() -> None:
             "gemm_a8w8": {"ms": round(t_gemm, 4), "TOPS": round(gemm_tops, 1)},
         },
     }
+    if not args.no_block:
+        del xq, w8, out
+        line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))
     if args.copy_probe:
         src = torch.full((args.copy_probe,), 1, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
