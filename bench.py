@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-block", action="store_true", help="skip the config-4 DiT block measurement")
     ap.add_argument("--block-steps", type=int, default=5)
+    ap.add_argument("--no-stream", action="store_true", help="skip the config-5 streamed 60-block stack")
+    ap.add_argument("--stream-blocks", type=int, default=60)
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="after the timed region, run 3 plain device-to-device copies of BYTES bytes: the reference "
@@ -151,6 +153,87 @@ def block_measurement(dev, steps: int, warmup: int):
                                     "sdpa": round(t_sdpa, 3), "rest": round(t_block - lin_ms - t_sdpa, 3)},
             "linears_int8_TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1),
             "sdpa_bf16_TFLOPS": round(sdpa_flop / (t_sdpa * 1e-3) / 1e12, 1)}
+
+
+def _config4_block_weights(dev, g):
+    """Random-init W4A8 weights of one config-4 block (GELU), made on the GPU: int4 codes uniform over the codebook
+    arange(-8, 8), group-128 fp16 scales in [12.875, 15.875], per-channel scale for ~N(0, 0.02) weights."""
+    import torch
+
+    from h3turbo_amd.types import BlockWeights, W4A8Weight
+
+    def lin(n, k):
+        q = torch.randint(-128, 128, (n, k // 2), generator=g, dtype=torch.int8, device=dev)
+        s_rel = (torch.rand(n, k // 128, generator=g, device=dev) * 3.0 + 12.875).to(torch.float16)
+        s_ch = torch.full((n,), 0.02 * 3 ** 0.5 / (7.5 * 14.375), device=dev)
+        return W4A8Weight(q, s_rel, s_ch, torch.arange(-8, 8, dtype=torch.float32, device=dev), group_size=128, convrot=256)
+
+    ones = lambda d: (1.0 + 0.1 * torch.randn(d, generator=g, device=dev))  # noqa: E731
+    return BlockWeights(qkv=lin(15360, 5120), out=lin(5120, 5120), fc1=lin(13824, 5120), fc2=lin(5120, 13824),
+                        norm1=ones(5120), norm2=ones(5120), q_norm=ones(128), k_norm=ones(128))
+
+
+def stream_measurement(dev, n_blocks: int):
+    """a stack of n_blocks config-4 blocks whose random-init W4A8 weights live in pinned host
+    RAM, run for one denoising step (12090 + 512 tokens) three ways: all resident in HBM (t_comp), streamed through
+    a 3-slot ring with 2-block lookahead on a side stream (t_both), and the copies alone (t_copy: every block
+    host -> HBM back to back).  overlap = (t_comp + t_copy - t_both) / min(t_comp, t_copy), the definition of the
+    reference's stream check (scripts/h3_check_stream_gpu.py:204-205).  The streamed output must equal the resident
+    output bit for bit."""
+    import torch
+
+    from h3turbo_amd import block as bk
+    from h3turbo_amd.blockstore import BlockLayout, HostBlockStore, block_tensors
+    from h3turbo_amd.stream import StreamingProvider, hip_transfer
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    t0 = time.perf_counter()
+    first = block_tensors(_config4_block_weights(dev, g))
+    store = HostBlockStore(BlockLayout.of(first), n_blocks, 128, 256, pinned=True)
+    store.write_block(0, first)
+    for i in range(1, n_blocks):
+        store.write_block(i, block_tensors(_config4_block_weights(dev, g)))
+    t_setup = time.perf_counter() - t0
+    s, hidden = 12602, 5120
+    cfg = bk.BlockConfig(hidden=hidden, heads=40, head_dim=128, ffn=13824, act="gelu")
+    x0 = torch.randn(s, hidden, generator=g, device=dev).to(torch.bfloat16)
+    mods = [torch.randn(1, hidden, generator=g, device=dev) * 0.1 for _ in range(6)]
+    pos = torch.stack(torch.meshgrid(torch.arange(31), torch.arange(15), torch.arange(26), indexing="ij"), -1).reshape(-1, 3)
+    pos = torch.cat([pos + 1, torch.zeros(512, 3, dtype=pos.dtype)], 0)
+    rope = bk.rope_tables(pos, 1.0 / (10000.0 ** (torch.arange(16) / 16.0)), dev, torch.bfloat16)
+    blk = bk.DiTBlock(cfg)
+
+    def forward_time(p):
+        bk.run_blocks(blk, x0.clone(), p, n_blocks, lambda i, w: mods, [(0, s, 0)], rope)  # warm (and prefetch)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        out = bk.run_blocks(blk, x0.clone(), p, n_blocks, lambda i, w: mods, [(0, s, 0)], rope)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t, out
+
+    with StreamingProvider(store, dev, resident=n_blocks) as p:
+        t_comp, out_res = forward_time(p)
+    with StreamingProvider(store, dev, resident=0, ring=3, prefetch=2) as p:
+        t_both, out_str = forward_time(p)
+        st = p.stats()
+    slot = torch.empty(store.block_nbytes, dtype=torch.uint8, device=dev)
+    cs = torch.cuda.Stream(dev)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(cs):
+        e0.record(cs)
+        for i in range(n_blocks):
+            hip_transfer(slot, store.block_tensor(i), True)
+        e1.record(cs)
+    torch.cuda.synchronize()
+    t_copy = e0.elapsed_time(e1) * 1e-3
+    overlap = (t_comp + t_copy - t_both) / min(t_comp, t_copy)
+    return {"config": f"{n_blocks} config-4 blocks (GELU, W4A8 g128 fp16 scales), S=12090+512, weights in pinned host RAM",
+            "block_MB": round(store.block_nbytes / 1e6, 1), "stack_GB": round(store.nbytes / 1e9, 2),
+            "resident_forward_s": round(t_comp, 4), "streamed_forward_s": round(t_both, 4), "copy_only_s": round(t_copy, 4),
+            "h2d_GB_per_s": round(store.nbytes / t_copy / 1e9, 1), "overlap": round(overlap, 3),
+            "streamed_equals_resident": bool(torch.equal(out_res, out_str)),
+            "waits": st["waits"], "host_kinds": st["host_kinds"], "setup_s": round(t_setup, 1)}
 
 
 def cpu_baseline(m: int, k: int, n: int, rows: int):
@@ -297,6 +380,8 @@ def main() -> None:
     if not args.no_block:
         del xq, w8, out
         line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))
+    if not args.no_stream:
+        line["stream"] = stream_measurement(dev, args.stream_blocks)
     if args.copy_probe:
         src = torch.full((args.copy_probe,), 1, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
