@@ -96,6 +96,18 @@ int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Per-head RMSNorm + split-half rotary embedding of q and k, in place, bf16.
+ * Replaces h3turbo/h3/layout.py:329-355 (norm_rope_, impl "torch": the numerics of comfy_kitchen's fused
+ * rms_rope_split_half_ called at :339, which the reference reproduces with rms_norm_fused_order, :309-326).
+ *   q, k     bf16 [tokens, heads, head_dim] with heads contiguous; ldq / ldk = elements between tokens
+ *   head_dim a multiple of 32 in [32, 256]; half = rotary pairs (2 * half <= head_dim)
+ *   wq, wk   fp32 [head_dim] norm weights; cos, sin fp32 [tokens, half], row stride ldcs; eps in fp32
+ */
+int h3k_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int64_t tokens, int heads, int head_dim,
+                     const float* wq, const float* wk, const float* cos, const float* sin, int64_t ldcs, int half,
+                     float eps, void* stream);
+
+/*
  * Host -> device copy of one weight block on the streaming engine's copy stream (hipMemcpyAsync).
  * Replaces the slot copy of h3turbo/h3/stream.py:346-354 (_issue: slot.buf.copy_(src, non_blocking)).
  * src is host memory (page-locked for an asynchronous copy), dst device memory.

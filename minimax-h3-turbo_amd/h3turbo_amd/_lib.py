@@ -33,6 +33,8 @@ SIGNATURES = {
     "h3k_w4a8_linear": (_int, [_ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _int, _i64, _ptr, _ptr, _i64, _int, _int,
                                _ptr, _int, _ptr, _int, _i64, _ptr, _size, _ptr]),
     "h3k_copy_h2d_async": (_int, [_ptr, _ptr, _size, _ptr]),
+    "h3k_qk_norm_rope": (_int, [_ptr, _i64, _ptr, _i64, _i64, _int, _int, _ptr, _ptr, _ptr, _ptr, _i64, _int,
+                                ctypes.c_float, _ptr]),
 }
 ABI_VERSION = 1
 

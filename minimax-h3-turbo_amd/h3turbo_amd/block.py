@@ -132,6 +132,9 @@ def norm_rope_(q: torch.Tensor, k: torch.Tensor, wq: torch.Tensor, wk: torch.Ten
     if impl not in ("torch", "eager"):
         raise ValueError(f"rope impl must be 'torch' or 'eager', got {impl!r}")
     half = cos.shape[1]
+    if impl == "torch" and _fused_norm_rope_ok(q, k):
+        _fused_norm_rope(q, k, wq, wk, eps, cos, sin)
+        return
     for t, w in ((q, wq), (k, wk)):
         for a in range(0, t.shape[0], chunk):
             rows = slice(a, a + chunk)
@@ -149,6 +152,25 @@ def norm_rope_(q: torch.Tensor, k: torch.Tensor, wq: torch.Tensor, wk: torch.Ten
             n[..., :half] = new_lo
             n[..., half:2 * half] = new_hi
             t[rows] = n
+
+
+def _fused_norm_rope_ok(q: torch.Tensor, k: torch.Tensor) -> bool:
+    d = q.shape[-1]
+    return (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and q.shape == k.shape
+            and d % 32 == 0 and d <= 256 and all(t.stride(2) == 1 and t.stride(1) == d for t in (q, k)))
+
+
+def _fused_norm_rope(q, k, wq, wk, eps, cos, sin) -> None:
+    """The same numerics in one HIP kernel over both tensors (h3k_qk_norm_rope)."""
+    from . import _lib
+
+    tokens, heads, d = q.shape
+    c, s = cos.float().contiguous(), sin.float().contiguous()
+    w_q, w_k = wq.float().contiguous(), wk.float().contiguous()
+    lib = _lib.load()
+    _lib.check(lib.h3k_qk_norm_rope(q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), tokens, heads, d,
+                                    w_q.data_ptr(), w_k.data_ptr(), c.data_ptr(), s.data_ptr(), c.shape[1], c.shape[1],
+                                    eps, _lib.stream_of(q.device)), "h3k_qk_norm_rope")
 
 
 # ------------------------------------------------------------------------------------------------ the block

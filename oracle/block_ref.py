@@ -94,6 +94,27 @@ def _rms_lanes(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return (xf * torch.rsqrt(acc / dd + eps) * w.float()).to(x.dtype)
 
 
+def norm_rope_ref(q: torch.Tensor, k: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, eps: float, cos: torch.Tensor,
+                  sin: torch.Tensor, impl: str = "torch") -> None:
+    """In place on [S, heads, D]: per-head RMSNorm then split-half rotation of the leading 2*half dims
+    (layout.py:329-355).  "torch": lane-order norm rounded to the dtype, rotation in fp32 (cos/sin widened), one
+    rounding.  "eager" (and fp32 inputs): F.rms_norm, rotation in the compute dtype.  Pinned by the reference's own
+    norm_rope_ outputs (tests/golden/make_golden_normrope.py)."""
+    half = cos.shape[1]
+    c, sn = cos.unsqueeze(1), sin.unsqueeze(1)
+    for t, g in ((q, wq), (k, wk)):
+        if impl == "eager" or t.dtype == torch.float32:
+            n = F.rms_norm(t, (t.shape[-1],), g.to(t.dtype), eps)
+            t1, t2 = n[..., :half], n[..., half:2 * half]
+            o1, o2 = (t1 * c).addcmul_(t2, -sn), (t2 * c).addcmul_(t1, sn)
+        else:
+            n = _rms_lanes(t, g, eps)
+            t1, t2 = n[..., :half].float(), n[..., half:2 * half].float()
+            o1, o2 = t1 * c.float() - t2 * sn.float(), t1 * sn.float() + t2 * c.float()
+        n[..., :half], n[..., half:2 * half] = o1, o2
+        t.copy_(n)
+
+
 def _modulate(h, shift, scale, segments):  # model.py:106-109
     for a, b, r in segments:
         h[a:b].mul_(1.0 + scale[r].to(h.dtype)).add_(shift[r].to(h.dtype))
@@ -112,19 +133,7 @@ def attend_ref(h: torch.Tensor, w: Dict[str, object], cos: torch.Tensor, sin: to
     dt, s, inner = h.dtype, h.shape[0], heads * head_dim
     qkv = _linear(h, w["qkv"], mode=mode)
     q, k, v = (t.reshape(s, heads, head_dim).clone() for t in qkv.split(inner, dim=-1))
-    half = cos.shape[1]
-    for t, g in ((q, w["q_norm"]), (k, w["k_norm"])):
-        c, sn = cos.unsqueeze(1), sin.unsqueeze(1)
-        if rope_impl == "eager" or dt == torch.float32:
-            n = F.rms_norm(t, (head_dim,), g.to(dt), qk_eps)
-            t1, t2 = n[..., :half], n[..., half:2 * half]
-            o1, o2 = (t1 * c).addcmul_(t2, -sn), (t2 * c).addcmul_(t1, sn)
-        else:
-            n = _rms_lanes(t, g, qk_eps)
-            t1, t2 = n[..., :half].float(), n[..., half:2 * half].float()
-            o1, o2 = t1 * c.float() - t2 * sn.float(), t1 * sn.float() + t2 * c.float()
-        n[..., :half], n[..., half:2 * half] = o1, o2
-        t.copy_(n)
+    norm_rope_ref(q, k, w["q_norm"], w["k_norm"], qk_eps, cos, sin, rope_impl)
     qf, kf, vf = (t.transpose(0, 1).float() for t in (q, k, v))
     att = torch.softmax((qf @ kf.transpose(1, 2)) / math.sqrt(head_dim), dim=-1)
     return (att @ vf).transpose(0, 1).reshape(s, inner).to(dt)

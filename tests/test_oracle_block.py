@@ -61,3 +61,28 @@ def test_w4a8_block_is_the_dense_block_within_activation_quantisation_noise(act)
     assert 1e-3 < r_delta < 4e-2, r_delta
     got16 = br.block_ref(x, {**lin, **norms}, mods, segs, cos, sin, SMALL["heads"], SMALL["head_dim"], act, 1e-5, 1e-5)
     assert rel(got16, want) < 1e-2
+
+
+# ------------------------------------------------------------------------------------------------ q/k norm + rope
+def _golden_normrope():
+    import fixtures as fx
+
+    return [n for n, m in fx.index().items() if m["kind"] == "normrope"]
+
+
+def _t16(a):
+    import numpy as np
+
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("name", _golden_normrope())
+def test_norm_rope_oracle_matches_the_reference_bit_for_bit(name):
+    import fixtures as fx
+
+    meta, a = fx.load(name)
+    q, k = _t16(a["q"]).clone(), _t16(a["k"]).clone()
+    br.norm_rope_ref(q, k, _t16(a["wq"]), _t16(a["wk"]), meta["eps"], _t16(a["cos"]), _t16(a["sin"]), meta["impl"])
+    assert torch.equal(q, _t16(a["q_out"])) and torch.equal(k, _t16(a["k_out"]))
+    if "q_norm_only" in a:
+        assert torch.equal(br._rms_lanes(_t16(a["q"]), _t16(a["wq"]), meta["eps"]), _t16(a["q_norm_only"]))
