@@ -157,6 +157,13 @@ __global__ __launch_bounds__(256, 1) void gemm_a8w8_kernel(const int8_t* __restr
 void gemm_pipe_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
                       const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo,
                       int32_t* acc_out, hipStream_t st);
+void gemm_persist_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
+                         const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo,
+                         int32_t* acc_out, hipStream_t st);
+
+#ifndef H3K_GEMM_PERSIST
+#define H3K_GEMM_PERSIST 1
+#endif
 
 template <int WMB, int WNB, int ODT, bool EAGER>
 static void launch_gemm(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k, const float* xs,
@@ -194,7 +201,11 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
   if (!aligned(a, 16) || lda % 16 || !aligned(w8, 16) || ldw % 16)
     return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
   const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
-  if (k % 64 == 0 && m > 512 && n >= 256)
+  const bool big = k % 64 == 0 && m > 512 && n >= 256;
+  if (H3K_GEMM_PERSIST && big && n % 4 == 0 && aligned(s_ch, 16) && aligned(xs, 16) &&
+      (bias == nullptr || aligned(bias, 16)))
+    gemm_persist_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
+  else if (big)
     gemm_pipe_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
   else if (m >= 2048 && n >= 256)
     launch_gemm_dt<4, 4>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);

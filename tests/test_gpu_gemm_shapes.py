@@ -1,0 +1,57 @@
+"""The large-shape GEMM kernels (persistent and pipelined, chosen by shape and alignment) against the CPU oracle
+on whole outputs: ragged M and N tails, K-step counts that do not divide the pipeline depth, every epilogue
+variant (ck / eager, bf16 / f16 / f32 out, bias, the int32 accumulator dump, unaligned output strides).  Bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from h3turbo_amd import _lib
+from oracle import qlinear_ref as ref
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+ODT = {_lib.BF16: (torch.bfloat16, "bf16"), _lib.F16: (torch.float16, "f16"), _lib.F32: (torch.float32, "f32")}
+
+
+def run(m, n, k, mode, odt, with_bias, ldo_pad=0, acc=False, seed=0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8, device=DEV)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8, device=DEV)
+    xs = torch.rand(m, generator=g, device=DEV) * 1e-2 + 1e-4
+    sch = torch.rand(n, generator=g, device=DEV) * 1e-2 + 1e-4
+    tdt, name = ODT[odt]
+    bias = (torch.randn(n, generator=g, device=DEV)).to(tdt) if with_bias else None
+    ldo = n + ldo_pad
+    out = torch.full((m, ldo), -7.0, dtype=tdt, device=DEV)
+    accb = torch.empty(m, n, dtype=torch.int32, device=DEV) if acc else None
+    lib = _lib.load()
+    _lib.check(lib.h3k_gemm_a8w8(a.data_ptr(), k, xs.data_ptr(), w.data_ptr(), k, sch.data_ptr(), _lib.ptr(bias), m, n, k,
+                                 _lib.MODE[mode], out.data_ptr(), odt, ldo, _lib.ptr(accb), _lib.stream_of(DEV)), "gemm")
+    torch.cuda.synchronize()
+    want_acc = ref.int8_mm(a.cpu().numpy(), w.cpu().numpy())
+    b = None if bias is None else bias.float().cpu().numpy()
+    want = ref.epilogue(want_acc, xs.cpu().numpy(), sch.cpu().numpy(), name, mode, b)
+    got = out[:, :n].float().cpu().numpy()
+    assert np.array_equal(got, want), f"outputs differ in {(got != want).sum()} places"
+    if ldo_pad:
+        assert (out[:, n:].float() == -7.0).all(), "wrote past the row"
+    if acc:
+        assert np.array_equal(accb.cpu().numpy(), want_acc)
+
+
+@pytest.mark.parametrize("m,n,k", [(1100, 520, 640), (700, 256, 64), (513, 1028, 1344), (2304, 768, 192)])
+def test_large_kernels_ragged_shapes_bf16(m, n, k):
+    print(f"gemm m={m} n={n} k={k}", flush=True)
+    run(m, n, k, "ck", _lib.BF16, False)
+
+
+@pytest.mark.parametrize("mode", ["ck", "eager"])
+@pytest.mark.parametrize("odt", [_lib.BF16, _lib.F16, _lib.F32])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_large_kernels_every_epilogue(mode, odt, with_bias):
+    run(1100, 520, 640, mode, odt, with_bias, seed=3)
+
+
+def test_large_kernels_accumulator_dump_and_unaligned_output_rows():
+    run(1100, 520, 640, "ck", _lib.BF16, True, ldo_pad=1, acc=True, seed=4)
+    run(1030, 772, 256, "eager", _lib.F32, False, ldo_pad=3, acc=True, seed=5)
