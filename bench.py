@@ -41,6 +41,7 @@ def parse():
     ap.add_argument("--no-block", action="store_true", help="skip the config-4 DiT block measurement")
     ap.add_argument("--block-steps", type=int, default=5)
     ap.add_argument("--no-stream", action="store_true", help="skip the config-5 streamed 60-block stack")
+    ap.add_argument("--sweep", action="store_true", help="add the config-3 GEMM sweep (16 shapes) to the line")
     ap.add_argument("--stream-blocks", type=int, default=60)
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -84,9 +85,10 @@ def synth_weight(n: int, k: int, dev, seed: int = 0, group: int = 128, convrot: 
 
 
 def gemm_kernel_name(m: int, n: int, k: int) -> str:
-    """The GEMM kernel h3k_gemm_a8w8 dispatches for this shape (the rule of gemm_a8w8_launch in h3k_gemm.hip)."""
+    """The GEMM kernel h3k_gemm_a8w8 dispatches for this shape with aligned operands (the rule of
+    gemm_a8w8_launch in h3k_gemm.hip)."""
     if k % 64 == 0 and m > 512 and n >= 256:
-        return "gemm_pipe_kernel"
+        return "gemm_persist_kernel" if n % 4 == 0 else "gemm_pipe_kernel"
     return "gemm_a8w8_kernel"
 
 
@@ -236,6 +238,60 @@ def stream_measurement(dev, n_blocks: int):
             "waits": st["waits"], "host_kinds": st["host_kinds"], "setup_s": round(t_setup, 1)}
 
 
+def sweep_measurement(dev, steps: int):
+    """the QLinear at M in {512, 4096, 12090, 32768} x (K, N) in {(5120, 5120), (5120, 15360),
+    (5120, 13824), (13824, 5120)}, weights of the BASELINE recipe.  Per shape: mean time of rotate+quant, decode,
+    GEMM (HIP events on the launch stream) and int8 TOPS of the GEMM and of the whole op."""
+    import torch
+
+    from h3turbo_amd import _lib
+    from h3turbo_amd import qlinear as ql
+    from h3turbo_amd.types import W4A8Weight
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    rows = []
+    for k, n in ((5120, 5120), (5120, 15360), (5120, 13824), (13824, 5120)):
+        q, s_rel, s_ch, cb = synth_weight(n, k, dev)
+        dw = ql._DevWeight(W4A8Weight(q, s_rel, s_ch, cb, group_size=128, convrot=256))
+        w8 = torch.empty(n, k, dtype=torch.int8, device=dev)
+        for m in (512, 4096, 12090, 32768):
+            g = torch.Generator(device=dev).manual_seed(m)
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            xq = torch.empty(m, k, dtype=torch.int8, device=dev)
+            xs = torch.empty(m, 1, dtype=torch.float32, device=dev)
+            out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            calls = [
+                lambda: lib.h3k_rotate_quant(x.data_ptr(), _lib.BF16, m, k, k, 256, 0, xq.data_ptr(), k, xs.data_ptr(), sp),
+                lambda: lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(), n, k,
+                                          128, w8.data_ptr(), k, sp),
+                lambda: lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, dw.s_ch.data_ptr(), None, m, n,
+                                          k, 0, out.data_ptr(), _lib.BF16, n, None, sp),
+            ]
+            for _ in range(2):
+                for c in calls:
+                    _lib.check(c(), "sweep")
+            ev = [[] for _ in calls]
+            for _ in range(steps):
+                for i, c in enumerate(calls):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    _lib.check(c(), "sweep")
+                    e1.record(stream)
+                    ev[i].append((e0, e1))
+            torch.cuda.synchronize()
+            t = [sum(a.elapsed_time(b) for a, b in e) / len(e) for e in ev]
+            ops = 2.0 * m * n * k
+            rows.append({"m": m, "k": k, "n": n, "rotquant_ms": round(t[0], 4), "decode_ms": round(t[1], 4),
+                         "gemm_ms": round(t[2], 4), "gemm_TOPS": round(ops / (t[2] * 1e-3) / 1e12, 1),
+                         "op_TOPS": round(ops / (sum(t) * 1e-3) / 1e12, 1),
+                         "gemm_frac_peak": round(ops / (t[2] * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)})
+            del x, xq, xs, out
+        del dw, w8
+    return rows
+
+
 def cpu_baseline(m: int, k: int, n: int, rows: int):
     """Time the CPU oracle (restatement of the reference's torch CPU backend) on `rows` rows of the workload plus
     one per-call weight decode, and scale to M rows: TOPS = 2MNK / (t_decode + t_rows * M / rows)."""
@@ -380,6 +436,8 @@ def main() -> None:
     if not args.no_block:
         del xq, w8, out
         line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))
+    if args.sweep:
+        line["sweep"] = sweep_measurement(dev, 10)
     if not args.no_stream:
         line["stream"] = stream_measurement(dev, args.stream_blocks)
     if args.copy_probe:

@@ -288,6 +288,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_persist_kernel(const int
 #define H3K_PERSIST_S 4
 #endif
 
+
 template <int ODT, bool EAGER>
 static void launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k, const float* xs,
                    const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, int grid, hipStream_t st) {

@@ -53,15 +53,20 @@ constexpr int kInStride = 16 * 16 + 16;  // uint16 per group: 16 rows of 16 + pa
 constexpr int kMidRow = 17;              // doubles per mid-transpose row (odd: conflict-free 64-bit access)
 constexpr int kMidStride = 16 * kMidRow + 4;
 
-template <int NPASS, bool F16, bool EAGER>
+// WPR wavefronts share a row (1 or 4): wave w of the row owns the 256-blocks (p * WPR + w) * 4 + g, so long rows
+// keep NPASS (and the registers holding the row) small; the row's absmax is then combined through LDS.
+template <int NPASS, int WPR, bool F16, bool EAGER>
 __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __restrict__ x, int64_t rows, int k,
                                                           int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
                                                           float* __restrict__ xs) {
+  static_assert(WPR == 1 || WPR == 4, "one row per wavefront or one row per workgroup");
   __shared__ __attribute__((aligned(16))) uint16_t s_in[4][4 * kInStride];
   __shared__ __attribute__((aligned(16))) double s_mid[4][4 * kMidStride];
+  __shared__ float s_amax[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-  if (row >= rows) return;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (4 / WPR) + wave / WPR;
+  const int wr = wave % WPR;
+  if (row >= rows) return;  // WPR == 4: the whole workgroup leaves together
   const int g = lane >> 4, l = lane & 15;
   const int nb = k >> 8;
   const uint16_t* xr = x + row * ldx;
@@ -69,7 +74,7 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
   u32x4 raw[NPASS][2];
 #pragma unroll
   for (int p = 0; p < NPASS; ++p) {
-    const int b = p * 4 + g;
+    const int b = (p * WPR + wr) * 4 + g;
     if (b < nb) {
       const u32x4* src = reinterpret_cast<const u32x4*>(xr + b * 256 + l * 16);
       raw[p][0] = __builtin_nontemporal_load(src);
@@ -87,7 +92,7 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
 
 #pragma unroll
   for (int p = 0; p < NPASS; ++p) {
-    const bool live = (p * 4 + g) < nb;
+    const bool live = ((p * WPR + wr) * 4 + g) < nb;
     // (1) transpose the 16-bit input: lane l then holds elements l + 16*r, r = 0..15 (digits 2,3 local)
     wave_lds_sync();
     *reinterpret_cast<u32x4*>(tin + l * 16) = raw[p][0];
@@ -130,8 +135,13 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
   }
 
   amax = wave_max(amax);
+  if (WPR > 1) {
+    if (lane == 0) s_amax[wave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(s_amax[0], s_amax[1]), fmaxf(s_amax[2], s_amax[3]));
+  }
   const float xsv = fmaxf(amax / 127.0f, 1e-30f);
-  if (lane == 0) xs[row] = xsv;
+  if (lane == 0 && wr == 0) xs[row] = xsv;
   float s = F16 ? round_f16(xsv) : round_bf16(xsv);
   if (s == 0.0f) s = F16 ? 6.103515625e-05f : 1.1754943508222875e-38f;
   // bf16: bf16(y * fl(1/s)) == bf16(fl(y / s)) for bf16 y, s (8-bit mantissas; checked exhaustively on the CPU)
@@ -140,7 +150,7 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
   int8_t* qr = q + row * ldq;
 #pragma unroll
   for (int p = 0; p < NPASS; ++p) {
-    const int b = p * 4 + g;
+    const int b = (p * WPR + wr) * 4 + g;
     if (b >= nb) continue;
     uint32_t packed[4];
 #pragma unroll
@@ -239,36 +249,47 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
 }
 
 // ------------------------------------------------------------------------------------------------ host side
-template <int NPASS, bool F16, bool EAGER>
+template <int NPASS, int WPR, bool F16, bool EAGER>
 static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int8_t* q, int64_t ldq, float* xs,
                       hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
-  hipLaunchKernelGGL((rotquant256_kernel<NPASS, F16, EAGER>), grid, dim3(256), 0, st,
+  const dim3 grid(static_cast<unsigned>((rows + (4 / WPR) - 1) / (4 / WPR)));
+  hipLaunchKernelGGL((rotquant256_kernel<NPASS, WPR, F16, EAGER>), grid, dim3(256), 0, st,
                      static_cast<const uint16_t*>(x), rows, k, ldx, q, ldq, xs);
 }
 
+#ifndef H3K_RQ_SPLIT_ABOVE
+#define H3K_RQ_SPLIT_ABOVE 8  // rows longer than this many passes of one wavefront are split over four
+#endif
+
+// blocks of 256 -> (passes, wavefronts per row); passes 0 when the row is too long for the fast kernel.  Few rows
+// (under 2048) are also split, to put more wavefronts on the chip.
+static void rq_plan(int blocks, int64_t rows, int& npass, int& wpr) {
+  static const int buckets[] = {1, 2, 3, 4, 5, 6, 7, 8};
+  wpr = ((blocks + 3) / 4 > H3K_RQ_SPLIT_ABOVE || (rows < 2048 && blocks > 4)) ? 4 : 1;
+  const int need = (blocks + 4 * wpr - 1) / (4 * wpr);
+  npass = 0;
+  for (int b : buckets)
+    if (b >= need) {
+      npass = b;
+      break;
+    }
+}
+
 template <bool F16, bool EAGER>
-static bool dispatch256(int npass, const void* x, int64_t rows, int k, int64_t ldx, int8_t* q, int64_t ldq, float* xs,
-                        hipStream_t st) {
-  switch (npass) {
-#define H3K_CASE(P) \
-  case P:           \
-    launch256<P, F16, EAGER>(x, rows, k, ldx, q, ldq, xs, st); \
+static bool dispatch256(int npass, int wpr, const void* x, int64_t rows, int k, int64_t ldx, int8_t* q, int64_t ldq,
+                        float* xs, hipStream_t st) {
+  switch (npass * 8 + wpr) {
+#define H3K_CASE(P, W)      \
+  case P * 8 + W:           \
+    launch256<P, W, F16, EAGER>(x, rows, k, ldx, q, ldq, xs, st); \
     return true;
-    H3K_CASE(1) H3K_CASE(2) H3K_CASE(3) H3K_CASE(4) H3K_CASE(5) H3K_CASE(6) H3K_CASE(7) H3K_CASE(8)
-    H3K_CASE(10) H3K_CASE(12) H3K_CASE(14) H3K_CASE(16)
+    H3K_CASE(1, 1) H3K_CASE(2, 1) H3K_CASE(3, 1) H3K_CASE(4, 1) H3K_CASE(5, 1) H3K_CASE(6, 1) H3K_CASE(7, 1)
+    H3K_CASE(8, 1) H3K_CASE(1, 4) H3K_CASE(2, 4) H3K_CASE(3, 4) H3K_CASE(4, 4) H3K_CASE(5, 4) H3K_CASE(6, 4)
+    H3K_CASE(7, 4) H3K_CASE(8, 4)
 #undef H3K_CASE
     default:
       return false;
   }
-}
-
-static int npass_bucket(int blocks) {
-  const int need = (blocks + 3) / 4;
-  static const int buckets[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
-  for (int b : buckets)
-    if (b >= need) return b;
-  return 0;
 }
 
 static int check_rot_args(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot) {
@@ -306,18 +327,19 @@ extern "C" int h3k_rotate_quant(const void* x, int x_dtype, int64_t rows, int64_
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool eager = mode == H3K_MODE_EAGER;
   const int es = x_dtype == H3K_F32 ? 4 : 2;
+  int np = 0, wpr = 1;
+  if (k <= (int64_t)256 * 128) rq_plan(static_cast<int>(k / 256), rows, np, wpr);
   const bool fast = rot == 256 && x_dtype != H3K_F32 && aligned(x, 16) && (ldx * es) % 16 == 0 && aligned(q, 16) &&
-                    ldq % 16 == 0 && npass_bucket(static_cast<int>(k / 256)) > 0;
+                    ldq % 16 == 0 && np > 0;
   if (fast) {
-    const int np = npass_bucket(static_cast<int>(k / 256));
     const int kk = static_cast<int>(k);
     bool ok;
     if (x_dtype == H3K_F16)
-      ok = eager ? dispatch256<true, true>(np, x, rows, kk, ldx, q, ldq, xs, st)
-                 : dispatch256<true, false>(np, x, rows, kk, ldx, q, ldq, xs, st);
+      ok = eager ? dispatch256<true, true>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st)
+                 : dispatch256<true, false>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st);
     else
-      ok = eager ? dispatch256<false, true>(np, x, rows, kk, ldx, q, ldq, xs, st)
-                 : dispatch256<false, false>(np, x, rows, kk, ldx, q, ldq, xs, st);
+      ok = eager ? dispatch256<false, true>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st)
+                 : dispatch256<false, false>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st);
     if (!ok) return fail(H3K_EINVAL, "no fast rotation kernel for k=%lld", (long long)k);
     return check_launch("rotquant256");
   }
