@@ -160,6 +160,7 @@ void gemm_pipe_launch(const int8_t* a, int64_t lda, const float* xs, const int8_
 void gemm_persist_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,
                          const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo,
                          int32_t* acc_out, hipStream_t st);
+int gemm_persist_min_k();
 
 #ifndef H3K_GEMM_PERSIST
 #define H3K_GEMM_PERSIST 1
@@ -202,7 +203,7 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
     return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
   const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
   const bool big = k % 64 == 0 && m > 512 && n >= 256;
-  if (H3K_GEMM_PERSIST && big && n % 4 == 0 && aligned(s_ch, 16) && aligned(xs, 16) &&
+  if (H3K_GEMM_PERSIST && big && n % 4 == 0 && k >= gemm_persist_min_k() && aligned(s_ch, 16) && aligned(xs, 16) &&
       (bias == nullptr || aligned(bias, 16)))
     gemm_persist_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
   else if (big)

@@ -1,6 +1,8 @@
 """The large-shape GEMM kernels (persistent and pipelined, chosen by shape and alignment) against the CPU oracle
 on whole outputs: ragged M and N tails, K-step counts that do not divide the pipeline depth, every epilogue
-variant (ck / eager, bf16 / f16 / f32 out, bias, the int32 accumulator dump, unaligned output strides).  Bit-exact."""
+variant (ck / eager, bf16 / f16 / f32 out, bias, the int32 accumulator dump, unaligned output strides), and grids
+where every persistent workgroup walks several tiles (full tiles only, and full tiles mixed with cut ones).
+Bit-exact."""
 import numpy as np
 import pytest
 import torch
@@ -50,6 +52,12 @@ def test_large_kernels_ragged_shapes_bf16(m, n, k):
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_large_kernels_every_epilogue(mode, odt, with_bias):
     run(1100, 520, 640, mode, odt, with_bias, seed=3)
+
+
+@pytest.mark.parametrize("m,n,k", [(6144, 8448, 512), (5000, 8000, 576)])
+def test_persistent_kernel_walks_several_tiles_per_workgroup(m, n, k):
+    print(f"gemm m={m} n={n} k={k}", flush=True)
+    run(m, n, k, "ck", _lib.BF16, False, seed=7)
 
 
 def test_large_kernels_accumulator_dump_and_unaligned_output_rows():
