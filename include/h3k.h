@@ -108,6 +108,44 @@ int h3k_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int64_t tokens,
                      float eps, void* stream);
 
 /*
+ * The block's attention prologue in one pass: per token and head, read the q, k and v head rows of the qkv
+ * projection output, apply h3k_qk_norm_rope's per-head RMSNorm + split-half rotation to q and k (the same
+ * arithmetic in the same order: bit-identical results), and write q, k, v head-major for the attention kernel.
+ * Replaces h3turbo/h3/model.py:196-214 (_attention: the qkv split, norm_rope_ at layout.py:329-355, and the
+ * [S, heads, D] -> [1, heads, S, D] layout the SDPA call at model.py:215-226 consumes).
+ *   qkv        bf16 [tokens, 3 * heads * head_dim] = (q | k | v), row stride ldqkv elements
+ *   head_dim   32, 64, 128 or 256; half, wq, wk, cos, sin, ldcs, eps as for h3k_qk_norm_rope
+ *   q/k/v_out  bf16 [heads, tokens, head_dim]: element (h, t, d) at out[h * head_stride + t * head_dim + d]
+ */
+int h3k_qkv_split_norm_rope(const void* qkv, int64_t ldqkv, int64_t tokens, int heads, int head_dim, const float* wq,
+                            const float* wk, const float* cos, const float* sin, int64_t ldcs, int half, float eps,
+                            void* q_out, void* k_out, void* v_out, int64_t head_stride, void* stream);
+
+/*
+ * h3k_rotate_quant over head-major rows: row r of the [rows, k] activation is the concatenation over heads h of
+ * x[h * head_stride + r * ldx + 0 .. head_dim-1] (the attention output [heads, tokens, head_dim] read as
+ * [tokens, heads * head_dim] without a transpose copy).  Same numerics and outputs as h3k_rotate_quant.
+ * Replaces the transpose + reshape of the attention output before the out projection
+ * (h3turbo/h3/model.py:226-228) together with the out projection's quantize_activation (qlinear.py:295-303).
+ *   bf16/f16 activations, rot = 256, head_dim a power of two >= 16 dividing k; x, q 16-byte aligned
+ */
+int h3k_rotate_quant_heads(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int head_dim,
+                           int64_t head_stride, int rot, int mode, int8_t* q, int64_t ldq, float* xs, void* stream);
+
+/*
+ * RMSNorm + AdaLN modulation of the residual stream in one pass, bf16:
+ *   n = bf16(x * rsqrt(mean(x^2) + eps) * w)  (fp32 math)    h = bf16(bf16(n * bf16(1 + scale[m])) + shift[m])
+ * with m = row_of_token[t] (NULL: row 0).  Replaces h3turbo/h3/model.py:64-65 (_rms) followed by :106-109
+ * (_scale_shift_), as _block applies them before the qkv and fc1 projections (:234-242).
+ *   x, h       bf16 [rows, k], row strides ldx / ldh; k a multiple of 8, at most 8192
+ *   w          bf16 [k] norm weight; shift, scale bf16 [R, k] modulation rows, row stride ldm
+ *   all pointers 16-byte aligned, strides multiples of 8 elements
+ */
+int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const void* w, const void* shift,
+                     const void* scale, int64_t ldm, const int32_t* row_of_token, float eps, void* h, int64_t ldh,
+                     void* stream);
+
+/*
  * Host -> device copy of one weight block on the streaming engine's copy stream (hipMemcpyAsync).
  * Replaces the slot copy of h3turbo/h3/stream.py:346-354 (_issue: slot.buf.copy_(src, non_blocking)).
  * src is host memory (page-locked for an asynchronous copy), dst device memory.

@@ -1,0 +1,106 @@
+// Token-wise ops of the DiT block around the W4A8 linears, fused: RMSNorm + AdaLN modulation in one pass.
+//
+// Reference h3turbo/h3/model.py:64-65 (_rms: F.rms_norm with the weight in x.dtype) and :106-109 (_scale_shift_:
+// h.mul_(1 + scale).add_(shift), in place in the activation dtype).  Per token row t (bf16, length k):
+//   r    = 1 / sqrt(sum_e fp32(x[e])^2 / k + eps)                   fp32; the sum's order is this kernel's own
+//   n[e] = bf16(fp32(x[e]) * r * w[e])                              F.rms_norm on bf16: fp32 math, one rounding
+//   h[e] = bf16(bf16(n[e] * bf16(1 + scale[m][e])) + shift[m][e])   m = the token's modulation row
+// One wavefront per row, the row held in registers (NV 16-byte chunks per lane), so x is read once and h written
+// once; w, shift and scale are the same for every row and come from L2.
+#include "h3k_common.hpp"
+
+namespace h3k {
+
+template <int NV>
+__global__ __launch_bounds__(256) void rms_modulate_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                           int k, const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ shift,
+                                                           const uint16_t* __restrict__ scale, int64_t ldm,
+                                                           const int32_t* __restrict__ row_of_token, float eps,
+                                                           uint16_t* __restrict__ h, int64_t ldh) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= rows) return;  // whole wavefronts
+  const uint16_t* xr = x + t * ldx;
+  u32x4 v[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e0 = (i * 64 + lane) * 8;
+    v[i] = e0 < k ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + e0)) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = __uint_as_float(v[i][j] << 16), b = __uint_as_float(v[i][j] & 0xFFFF0000u);
+      ss = ss + fp32_round_point(a * a);
+      ss = ss + fp32_round_point(b * b);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
+  const float r = 1.0f / sqrtf(fp32_round_point(fp32_round_point(ss / static_cast<float>(k)) + eps));
+  const int64_t m = row_of_token ? row_of_token[t] : 0;
+  const uint16_t* sh = shift + m * ldm;
+  const uint16_t* sc = scale + m * ldm;
+  uint16_t* hr = h + t * ldh;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e0 = (i * 64 + lane) * 8;
+    if (e0 >= k) continue;
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + e0);
+    const u32x4 shv = *reinterpret_cast<const u32x4*>(sh + e0);
+    const u32x4 scv = *reinterpret_cast<const u32x4*>(sc + e0);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int sft = 16 * half;
+        const float xe = bf16_to_f32((v[i][j] >> sft) & 0xFFFFu);
+        const float we = bf16_to_f32((wv[j] >> sft) & 0xFFFFu);
+        const float n = round_bf16(fp32_round_point(fp32_round_point(xe * r) * we));
+        const float one_plus = round_bf16(bf16_to_f32((scv[j] >> sft) & 0xFFFFu) + 1.0f);
+        const float h1 = round_bf16(fp32_round_point(n * one_plus));
+        const float h2 = fp32_round_point(h1 + bf16_to_f32((shv[j] >> sft) & 0xFFFFu));
+        word |= f32_to_bf16_bits(h2) << sft;
+      }
+      o[j] = word;
+    }
+    *reinterpret_cast<u32x4*>(hr + e0) = o;
+  }
+}
+
+}  // namespace h3k
+
+using namespace h3k;
+
+extern "C" int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const void* w, const void* shift,
+                                const void* scale, int64_t ldm, const int32_t* row_of_token, float eps, void* h,
+                                int64_t ldh, void* stream) {
+  if (rows < 0 || k <= 0 || k % 8 || k > 16 * 512)
+    return fail(H3K_EINVAL, "k=%lld must be a positive multiple of 8 up to 8192", (long long)k);
+  if (ldx < k || ldh < k || ldm < k) return fail(H3K_EINVAL, "row strides smaller than the rows");
+  if (rows == 0) return H3K_OK;
+  if (!x || !w || !shift || !scale || !h) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(shift, 16) || !aligned(scale, 16) || !aligned(h, 16) || ldx % 8 ||
+      ldh % 8 || ldm % 8)
+    return fail(H3K_EINVAL, "rows and vectors must be 16-byte aligned (strides multiples of 8 elements)");
+  const int nv = static_cast<int>((k + 511) / 512);
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t *xp = static_cast<const uint16_t*>(x), *wp = static_cast<const uint16_t*>(w);
+  const uint16_t *shp = static_cast<const uint16_t*>(shift), *scp = static_cast<const uint16_t*>(scale);
+  uint16_t* hp = static_cast<uint16_t*>(h);
+  const int kk = static_cast<int>(k);
+  switch (nv) {
+#define H3K_RM(NV)                                                                                                \
+  case NV:                                                                                                        \
+    hipLaunchKernelGGL((rms_modulate_kernel<NV>), grid, dim3(256), 0, st, xp, ldx, rows, kk, wp, shp, scp, ldm,    \
+                       row_of_token, eps, hp, ldh);                                                               \
+    break;
+    H3K_RM(1) H3K_RM(2) H3K_RM(3) H3K_RM(4) H3K_RM(5) H3K_RM(6) H3K_RM(7) H3K_RM(8) H3K_RM(9) H3K_RM(10) H3K_RM(11)
+    H3K_RM(12) H3K_RM(13) H3K_RM(14) H3K_RM(15) H3K_RM(16)
+#undef H3K_RM
+  }
+  return check_launch("rms_modulate");
+}

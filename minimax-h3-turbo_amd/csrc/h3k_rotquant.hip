@@ -55,10 +55,13 @@ constexpr int kMidStride = 16 * kMidRow + 4;
 
 // WPR wavefronts share a row (1 or 4): wave w of the row owns the 256-blocks (p * WPR + w) * 4 + g, so long rows
 // keep NPASS (and the registers holding the row) small; the row's absmax is then combined through LDS.
+// Row layout: element e of row r is at x[r * ldx + (e >> hshift) * hstride + (e & (2^hshift - 1))]; hshift = 31
+// is a plain row, hshift = log2(head_dim) reads a head-major [heads, rows, head_dim] tensor as rows of
+// heads * head_dim (head_dim >= 16, so a lane's 16 consecutive elements stay inside one head).
 template <int NPASS, int WPR, bool F16, bool EAGER>
 __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __restrict__ x, int64_t rows, int k,
-                                                          int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
-                                                          float* __restrict__ xs) {
+                                                          int64_t ldx, int hshift, int64_t hstride,
+                                                          int8_t* __restrict__ q, int64_t ldq, float* __restrict__ xs) {
   static_assert(WPR == 1 || WPR == 4, "one row per wavefront or one row per workgroup");
   __shared__ __attribute__((aligned(16))) uint16_t s_in[4][4 * kInStride];
   __shared__ __attribute__((aligned(16))) double s_mid[4][4 * kMidStride];
@@ -76,7 +79,9 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
   for (int p = 0; p < NPASS; ++p) {
     const int b = (p * WPR + wr) * 4 + g;
     if (b < nb) {
-      const u32x4* src = reinterpret_cast<const u32x4*>(xr + b * 256 + l * 16);
+      const int e = b * 256 + l * 16;
+      const u32x4* src = reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(e >> hshift) * hstride +
+                                                        (e & ((1 << hshift) - 1)));
       raw[p][0] = __builtin_nontemporal_load(src);
       raw[p][1] = __builtin_nontemporal_load(src + 1);
     } else {
@@ -250,11 +255,11 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
 
 // ------------------------------------------------------------------------------------------------ host side
 template <int NPASS, int WPR, bool F16, bool EAGER>
-static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int8_t* q, int64_t ldq, float* xs,
-                      hipStream_t st) {
+static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int hshift, int64_t hstride, int8_t* q,
+                      int64_t ldq, float* xs, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>((rows + (4 / WPR) - 1) / (4 / WPR)));
   hipLaunchKernelGGL((rotquant256_kernel<NPASS, WPR, F16, EAGER>), grid, dim3(256), 0, st,
-                     static_cast<const uint16_t*>(x), rows, k, ldx, q, ldq, xs);
+                     static_cast<const uint16_t*>(x), rows, k, ldx, hshift, hstride, q, ldq, xs);
 }
 
 #ifndef H3K_RQ_SPLIT_ABOVE
@@ -276,12 +281,12 @@ static void rq_plan(int blocks, int64_t rows, int& npass, int& wpr) {
 }
 
 template <bool F16, bool EAGER>
-static bool dispatch256(int npass, int wpr, const void* x, int64_t rows, int k, int64_t ldx, int8_t* q, int64_t ldq,
-                        float* xs, hipStream_t st) {
+static bool dispatch256(int npass, int wpr, const void* x, int64_t rows, int k, int64_t ldx, int hshift,
+                        int64_t hstride, int8_t* q, int64_t ldq, float* xs, hipStream_t st) {
   switch (npass * 8 + wpr) {
 #define H3K_CASE(P, W)      \
   case P * 8 + W:           \
-    launch256<P, W, F16, EAGER>(x, rows, k, ldx, q, ldq, xs, st); \
+    launch256<P, W, F16, EAGER>(x, rows, k, ldx, hshift, hstride, q, ldq, xs, st); \
     return true;
     H3K_CASE(1, 1) H3K_CASE(2, 1) H3K_CASE(3, 1) H3K_CASE(4, 1) H3K_CASE(5, 1) H3K_CASE(6, 1) H3K_CASE(7, 1)
     H3K_CASE(8, 1) H3K_CASE(1, 4) H3K_CASE(2, 4) H3K_CASE(3, 4) H3K_CASE(4, 4) H3K_CASE(5, 4) H3K_CASE(6, 4)
@@ -335,11 +340,11 @@ extern "C" int h3k_rotate_quant(const void* x, int x_dtype, int64_t rows, int64_
     const int kk = static_cast<int>(k);
     bool ok;
     if (x_dtype == H3K_F16)
-      ok = eager ? dispatch256<true, true>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st)
-                 : dispatch256<true, false>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st);
+      ok = eager ? dispatch256<true, true>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st)
+                 : dispatch256<true, false>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st);
     else
-      ok = eager ? dispatch256<false, true>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st)
-                 : dispatch256<false, false>(np, wpr, x, rows, kk, ldx, q, ldq, xs, st);
+      ok = eager ? dispatch256<false, true>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st)
+                 : dispatch256<false, false>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st);
     if (!ok) return fail(H3K_EINVAL, "no fast rotation kernel for k=%lld", (long long)k);
     return check_launch("rotquant256");
   }
@@ -356,6 +361,44 @@ extern "C" int h3k_rotate_quant(const void* x, int x_dtype, int64_t rows, int64_
   }
 #undef H3K_GEN
   return check_launch("rot_generic(quant)");
+}
+
+extern "C" int h3k_rotate_quant_heads(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                                      int head_dim, int64_t head_stride, int rot, int mode, int8_t* q, int64_t ldq,
+                                      float* xs, void* stream) {
+  if (x_dtype != H3K_BF16 && x_dtype != H3K_F16 && x_dtype != H3K_F32)
+    return fail(H3K_EINVAL, "activations must be bf16, f16 or f32 (dtype code %d)", x_dtype);
+  if (rows < 0 || ldx < head_dim) return fail(H3K_EINVAL, "rows=%lld, ldx=%lld < head_dim=%d", (long long)rows,
+                                              (long long)ldx, head_dim);
+  if (x_dtype == H3K_F32 || rot != 256)
+    return fail(H3K_EINVAL, "head-major rows take bf16/f16 activations and rotation 256 (dtype %d, rot %d)", x_dtype, rot);
+  if (mode != H3K_MODE_CK && mode != H3K_MODE_EAGER) return fail(H3K_EINVAL, "mode must be ck (0) or eager (1)");
+  if (head_dim < 16 || (head_dim & (head_dim - 1)) || k % head_dim || k <= 0 || k % 256)
+    return fail(H3K_EINVAL, "head_dim=%d must be a power of two >= 16 dividing k=%lld (a multiple of 256)", head_dim,
+                (long long)k);
+  if (head_stride < rows * ldx) return fail(H3K_EINVAL, "head_stride < rows * ldx (heads overlap)");
+  if (ldq < k) return fail(H3K_EINVAL, "ldq=%lld < k=%lld", (long long)ldq, (long long)k);
+  if (rows == 0) return H3K_OK;
+  if (!x || !q || !xs) return fail(H3K_EINVAL, "x/q/xs is NULL");
+  if (!aligned(x, 16) || (ldx * 2) % 16 || (head_stride * 2) % 16 || !aligned(q, 16) || ldq % 16)
+    return fail(H3K_EINVAL, "x / q and their strides must be 16-byte aligned");
+  int np = 0, wpr = 1;
+  if (k <= (int64_t)256 * 128) rq_plan(static_cast<int>(k / 256), rows, np, wpr);
+  if (np == 0) return fail(H3K_EINVAL, "k=%lld too long for head-major rows", (long long)k);
+  int hshift = 0;
+  while ((1 << hshift) < head_dim) ++hshift;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool eager = mode == H3K_MODE_EAGER;
+  const int kk = static_cast<int>(k);
+  bool ok;
+  if (x_dtype == H3K_F16)
+    ok = eager ? dispatch256<true, true>(np, wpr, x, rows, kk, ldx, hshift, head_stride, q, ldq, xs, st)
+               : dispatch256<true, false>(np, wpr, x, rows, kk, ldx, hshift, head_stride, q, ldq, xs, st);
+  else
+    ok = eager ? dispatch256<false, true>(np, wpr, x, rows, kk, ldx, hshift, head_stride, q, ldq, xs, st)
+               : dispatch256<false, false>(np, wpr, x, rows, kk, ldx, hshift, head_stride, q, ldq, xs, st);
+  if (!ok) return fail(H3K_EINVAL, "no fast rotation kernel for k=%lld", (long long)k);
+  return check_launch("rotquant256(heads)");
 }
 
 extern "C" int h3k_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot, void* y,

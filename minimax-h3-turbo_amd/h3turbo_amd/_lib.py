@@ -35,6 +35,10 @@ SIGNATURES = {
     "h3k_copy_h2d_async": (_int, [_ptr, _ptr, _size, _ptr]),
     "h3k_qk_norm_rope": (_int, [_ptr, _i64, _ptr, _i64, _i64, _int, _int, _ptr, _ptr, _ptr, _ptr, _i64, _int,
                                 ctypes.c_float, _ptr]),
+    "h3k_qkv_split_norm_rope": (_int, [_ptr, _i64, _i64, _int, _int, _ptr, _ptr, _ptr, _ptr, _i64, _int, ctypes.c_float,
+                                       _ptr, _ptr, _ptr, _i64, _ptr]),
+    "h3k_rotate_quant_heads": (_int, [_ptr, _int, _i64, _i64, _i64, _int, _i64, _int, _int, _ptr, _i64, _ptr, _ptr]),
+    "h3k_rms_modulate": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr, ctypes.c_float, _ptr, _i64, _ptr]),
 }
 ABI_VERSION = 1
 

@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import qlinear
-from .types import BlockProvider, BlockWeights, Weight
+from .types import BlockProvider, BlockWeights, W4A8Weight, Weight
 
 # a modulation segment: tokens [start, stop) use row `row` (an int, or a LongTensor of per-token rows)
 Segment = Tuple[int, int, Union[int, torch.Tensor]]
@@ -82,6 +82,45 @@ def modulate_(h: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, segment
     for a, b, row in _row_pieces(segments):
         one_plus = scale[row].to(h.dtype) + 1.0
         h[a:b].mul_(one_plus).add_(shift[row].to(h.dtype))
+    return h
+
+
+def token_rows(segments: Sequence[Segment], s: int, device) -> Optional[torch.Tensor]:
+    """The modulation row of every token as int32 [s] on `device`, or None when the segments do not cover
+    [0, s) contiguously (tokens outside every segment stay unmodulated, which the fused kernel cannot express)."""
+    pos = 0
+    rows = torch.empty(s, dtype=torch.int32, device=device)
+    for start, stop, row in segments:
+        if start != pos or stop < start:
+            return None
+        rows[start:stop] = row.to(device=device, dtype=torch.int32) if isinstance(row, torch.Tensor) else int(row)
+        pos = stop
+    return rows if pos == s else None
+
+
+def rms_modulate(x: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float,
+                 segments: Sequence[Segment], rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """modulate_(rms(x, weight, eps), shift, scale, segments) (h3turbo/h3/model.py:64-65, 106-109), in one HIP pass
+    (h3k_rms_modulate) for bf16 on the GPU when the segments cover every token; `rows` is token_rows(segments)
+    when already built.  The fused pass sums the squares in its own order, so it can differ from F.rms_norm in the
+    last bit of the norm on some rows."""
+    k = x.shape[-1]
+    fused = (x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and k % 8 == 0 and k <= 8192
+             and x.stride(-1) == 1 and (x.shape[0] <= 1 or x.stride(0) % 8 == 0) and x.data_ptr() % 16 == 0)
+    if fused and rows is None:
+        rows = token_rows(segments, x.shape[0], x.device)
+    if not fused or rows is None or shift.shape[-1] != k or scale.shape[-1] != k:
+        return modulate_(rms(x, weight, eps), shift, scale, segments)
+    from . import _lib
+
+    h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    w = weight.to(x.dtype).contiguous()
+    sh = shift.reshape(-1, k).to(x.dtype).contiguous()
+    sc = scale.reshape(-1, k).to(x.dtype).contiguous()
+    lib = _lib.load()
+    _lib.check(lib.h3k_rms_modulate(x.data_ptr(), x.stride(0) if x.shape[0] > 1 else k, x.shape[0], k, w.data_ptr(),
+                                    sh.data_ptr(), sc.data_ptr(), k, rows.data_ptr(), eps, h.data_ptr(), k,
+                                    _lib.stream_of(x.device)), "h3k_rms_modulate")
     return h
 
 
@@ -173,6 +212,35 @@ def _fused_norm_rope(q, k, wq, wk, eps, cos, sin) -> None:
                                     eps, _lib.stream_of(q.device)), "h3k_qk_norm_rope")
 
 
+def _split_norm_rope_ok(qkv: torch.Tensor, heads: int, head_dim: int, rope) -> bool:
+    """The fused split kernel's preconditions: bf16 rows with a contiguous last dim, each lane's head_dim/16-byte
+    access aligned."""
+    vb = head_dim // 16
+    return (rope is not None and qkv.is_cuda and qkv.dtype == torch.bfloat16 and head_dim in (32, 64, 128, 256)
+            and qkv.stride(-1) == 1 and qkv.shape[-1] == 3 * heads * head_dim and qkv.data_ptr() % vb == 0
+            and (qkv.shape[0] <= 1 or (2 * qkv.stride(0)) % vb == 0))
+
+
+def qkv_split_norm_rope(qkv: torch.Tensor, heads: int, head_dim: int, wq: torch.Tensor, wk: torch.Tensor, eps: float,
+                        cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """The qkv projection output [S, 3 * heads * head_dim] -> head-major [3, heads, S, head_dim] (q, k, v) with the
+    "torch" norm + rope applied to q and k, in one HIP kernel (h3k_qkv_split_norm_rope).  Bit-identical to
+    splitting, norm_rope_(q, k, ..., impl="torch") and transposing each part to [heads, S, head_dim]
+    (h3turbo/h3/model.py:196-214, layout.py:329-355)."""
+    from . import _lib
+
+    s = qkv.shape[0]
+    out = torch.empty(3, heads, s, head_dim, dtype=qkv.dtype, device=qkv.device)
+    c, sn = cos.float().contiguous(), sin.float().contiguous()
+    w_q, w_k = wq.float().contiguous(), wk.float().contiguous()
+    lib = _lib.load()
+    _lib.check(lib.h3k_qkv_split_norm_rope(qkv.data_ptr(), qkv.stride(0) if s > 1 else qkv.shape[1], s, heads, head_dim,
+                                           w_q.data_ptr(), w_k.data_ptr(), c.data_ptr(), sn.data_ptr(), c.shape[1],
+                                           c.shape[1], eps, out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
+                                           s * head_dim, _lib.stream_of(qkv.device)), "h3k_qkv_split_norm_rope")
+    return out
+
+
 # ------------------------------------------------------------------------------------------------ the block
 class DiTBlock:
     """Runs H3 DiT blocks on the GPU with W4A8 (or dense) linears.
@@ -223,13 +291,35 @@ class DiTBlock:
 
     def attention(self, h: torch.Tensor, w: BlockWeights, rope: Optional[Tuple[torch.Tensor, torch.Tensor]]) -> torch.Tensor:
         """out(SDPA(norm_rope(q), norm_rope(k), v)) (h3turbo/h3/model.py:196-228).  rope None: plain per-head norm."""
-        return self.linear(self.attend(h, w, rope), w.out)
+        o = self.attend(h, w, rope, head_major=self._fused_attention(w))
+        if o.dim() == 3:  # head-major [heads, S, head_dim]: the out projection reads it without a transpose copy
+            return qlinear.linear_heads(o, w.out, quant_mode=self.quant_mode)
+        return self.linear(o, w.out)
 
-    def attend(self, h: torch.Tensor, w: BlockWeights, rope: Optional[Tuple[torch.Tensor, torch.Tensor]]) -> torch.Tensor:
-        """The attention output before the out projection: [S, heads * head_dim] in h.dtype."""
+    def _fused_attention(self, w: BlockWeights) -> bool:
+        """Whether the attention runs on the fused HIP prologue / epilogue (split + norm + rope into head-major
+        q, k, v; the out projection reading the head-major attention output): W4A8 a8 linears, "torch" rope."""
+        return (isinstance(w.qkv, W4A8Weight) and isinstance(w.out, W4A8Weight) and self.precision == "a8"
+                and self.rope_impl == "torch" and self.cfg.head_dim in (32, 64, 128, 256))
+
+    def attend(self, h: torch.Tensor, w: BlockWeights, rope: Optional[Tuple[torch.Tensor, torch.Tensor]],
+               head_major: bool = False) -> torch.Tensor:
+        """The attention output before the out projection: [S, heads * head_dim] in h.dtype, or with head_major
+        (and the fused prologue applicable) [heads, S, head_dim]."""
         cfg = self.cfg
         s = h.shape[0]
         qkv = self.linear(h, w.qkv)
+        if head_major and _split_norm_rope_ok(qkv, cfg.heads, cfg.head_dim, rope):
+            qkvh = qkv_split_norm_rope(qkv, cfg.heads, cfg.head_dim, w.q_norm, w.k_norm, cfg.qk_norm_eps, rope[0], rope[1])
+            del qkv
+            qh, kh, vh = (qkvh[i].unsqueeze(0) for i in range(3))
+            step = self.attn_chunk or s
+            if step >= s:
+                return _sdpa(qh, kh, vh)[0]
+            o = torch.empty(cfg.heads, s, cfg.head_dim, dtype=h.dtype, device=h.device)
+            for a in range(0, s, step):
+                o[:, a:a + step] = _sdpa(qh[:, :, a:a + step], kh, vh)[0]
+            return o
         q, k, v = (t.view(s, cfg.heads, cfg.head_dim) for t in qkv.split(cfg.inner, dim=-1))
         if rope is None:
             q, k = rms(q, w.q_norm, cfg.qk_norm_eps), rms(k, w.k_norm, cfg.qk_norm_eps)
@@ -265,9 +355,10 @@ class DiTBlock:
             raise ValueError(f"a DiT block takes 6 modulation tensors, got {len(mods)}")
         sh_a, sc_a, g_a, sh_m, sc_m, g_m = mods
         eps = self.cfg.norm_eps
-        h = modulate_(rms(x, w.norm1, eps), sh_a, sc_a, segments)
+        rows = token_rows(segments, x.shape[0], x.device) if x.is_cuda else None
+        h = rms_modulate(x, w.norm1, sh_a, sc_a, eps, segments, rows)
         gated_add_(x, g_a, self.attention(h, w, rope), segments)
-        h = modulate_(rms(x, w.norm2, eps), sh_m, sc_m, segments)
+        h = rms_modulate(x, w.norm2, sh_m, sc_m, eps, segments, rows)
         return gated_add_(x, g_m, self.mlp(h, w), segments)
 
     __call__ = forward

@@ -253,12 +253,16 @@ class _HipRunner:
         (self._a8 if self.precision == "a8" else self._a16)(x2, out)
 
     def _a8(self, x2: torch.Tensor, out: torch.Tensor) -> None:
-        m = x2.shape[0]
         xq, xs = _quantize_rows(x2, self.w.convrot, self.mode)
+        self.gemm(xq, xs, out)
+
+    def gemm(self, xq: torch.Tensor, xs: torch.Tensor, out: torch.Tensor) -> None:
+        """The int8 GEMM with the fused epilogue on quantised activations xq [m, K], scales xs [m, 1]."""
+        m = xq.shape[0]
         _lib.check(self.lib.h3k_gemm_a8w8(xq.data_ptr(), self.k, xs.data_ptr(), self.w8.data_ptr(), self.k,
                                           self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
                                           _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0), None,
-                                          _lib.stream_of(x2.device)), "h3k_gemm_a8w8")
+                                          _lib.stream_of(xq.device)), "h3k_gemm_a8w8")
 
     def _a16(self, x2: torch.Tensor, out: torch.Tensor) -> None:
         """Unquantised activation (qlinear.py:407-424): rotated x (rounded to x.dtype) times the exact int8 levels
@@ -296,6 +300,43 @@ def _linear_w4a8(x2, w, bias, out_dtype, backend, precision, swiglu, chunk_token
         if swiglu:
             xc = _swiglu(xc)
         runner(xc, out[a: a + step])
+    return out
+
+
+@torch.no_grad()
+def linear_heads(xh: torch.Tensor, w: W4A8Weight, *, out_dtype: Optional[torch.dtype] = None,
+                 quant_mode: str = "ck") -> torch.Tensor:
+    """linear(x, w) for x given head-major: xh [heads, tokens, head_dim] is read as x [tokens, heads * head_dim]
+    (row t = concatenation over heads of xh[h, t]) without materialising the transpose.  This is the attention
+    output feeding the out projection (h3turbo/h3/model.py:226-228: transpose + reshape, then _matmul).  W4A8 a8
+    on the HIP kernels only; bit-identical to linear(xh.transpose(0, 1).reshape(tokens, -1), w)."""
+    _check_mode(quant_mode)
+    if xh.dim() != 3:
+        raise ValueError(f"xh must be [heads, tokens, head_dim], got {tuple(xh.shape)}")
+    heads, m, hd = xh.shape
+    n, k = _check_weight(w)
+    if heads * hd != k:
+        raise ValueError(f"input features {heads * hd} do not match the weight's K={k}")
+    if xh.device != w.q.device:
+        raise ValueError(f"input on {xh.device} but weight on {w.q.device}")
+    out_dtype = out_dtype or xh.dtype
+    if m == 0:
+        return torch.empty(0, n, dtype=out_dtype, device=xh.device)
+    _need_gpu(xh, "linear_heads")
+    if xh.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"linear_heads takes bf16 or f16 activations, got {xh.dtype}")
+    if xh.stride(2) != 1 or xh.stride(1) < hd or (heads > 1 and xh.stride(0) < m * xh.stride(1)):
+        xh = xh.contiguous()
+    ldx, hstride = xh.stride(1), (xh.stride(0) if heads > 1 else m * xh.stride(1))
+    runner = _HipRunner(w, None, out_dtype, "a8", quant_mode)
+    q = torch.empty(m, k, dtype=torch.int8, device=xh.device)
+    xs = torch.empty(m, 1, dtype=torch.float32, device=xh.device)
+    lib = _lib.load()
+    _lib.check(lib.h3k_rotate_quant_heads(xh.data_ptr(), _lib.act_code(xh.dtype), m, k, ldx, hd, hstride, w.convrot,
+                                          _lib.MODE[quant_mode], q.data_ptr(), k, xs.data_ptr(),
+                                          _lib.stream_of(xh.device)), "h3k_rotate_quant_heads")
+    out = torch.empty(m, n, dtype=out_dtype, device=xh.device)
+    runner.gemm(q, xs, out)
     return out
 
 

@@ -203,3 +203,30 @@ def _config4_weights(hidden, inner, fc1_out, ffn, g) -> BlockWeights:
     ones = lambda d: 1.0 + 0.1 * torch.randn(d, generator=g, device=DEV)  # noqa: E731
     return BlockWeights(qkv=lin(3 * inner, hidden), out=lin(hidden, inner), fc1=lin(fc1_out, hidden), fc2=lin(hidden, ffn),
                         norm1=ones(hidden), norm2=ones(hidden), q_norm=ones(128), k_norm=ones(128))
+
+
+@pytest.mark.parametrize("s,k,int_valued", [(37, 5120, True), (300, 1024, True), (5, 5376, True), (129, 5120, False)])
+def test_fused_rms_modulate_matches_the_torch_ops(s, k, int_valued):
+    """h3k_rms_modulate against F.rms_norm + the in-place modulation on the CPU (h3turbo/h3/model.py:64-65,
+    106-109).  With integer-valued rows the sum of squares is exact in any order and the outputs are bit-exact;
+    on Gaussian rows the kernel's own summation order may move the norm by an ulp on a few rows."""
+    print(f"rms_modulate s={s} k={k} int={int_valued}", flush=True)
+    g = torch.Generator().manual_seed(s + k)
+    if int_valued:
+        x = torch.randint(-8, 9, (s, k), generator=g).to(torch.bfloat16)
+    else:
+        x = (torch.randn(s, k, generator=g) * torch.exp(torch.randn(s, 1, generator=g))).to(torch.bfloat16)
+    w = 1 + 0.2 * torch.randn(k, generator=g)
+    shift, scale = 0.1 * torch.randn(3, k, generator=g), 0.1 * torch.randn(3, k, generator=g)
+    a, b = s // 3, 2 * s // 3
+    segments = [(0, a, 0), (a, b, torch.randint(0, 3, (b - a,), generator=g)), (b, s, 2)]
+    want = bk.modulate_(bk.rms(x, w, 1e-5), shift, scale, segments)
+    seg_gpu = [(p, q, r.to(DEV) if isinstance(r, torch.Tensor) else r) for p, q, r in segments]
+    got = bk.rms_modulate(x.to(DEV), w.to(DEV), shift.to(DEV), scale.to(DEV), 1e-5, seg_gpu).cpu()
+    if int_valued:
+        assert torch.equal(got, want)
+    else:
+        diff = (got.float() - want.float()).abs()
+        ulp = want.float().abs().clamp_min(1e-30) * 2.0 ** -7
+        assert (diff <= ulp * 1.01 + 1e-30).all(), "more than one bf16 ulp away"
+        assert (got != want).float().mean().item() < 0.01

@@ -386,3 +386,22 @@ def test_epilogue_matches_the_oracle_on_random_accumulators(mode, odt):
     assert np.array_equal(acc.cpu().numpy(), want_acc)
     want = ref.epilogue(want_acc, xs.numpy(), sc.numpy(), name, mode, bias.float().numpy())
     assert np.array_equal(out.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("heads,hd,m,n", [(40, 128, 300, 256), (4, 64, 33, 72), (2, 256, 7, 40), (16, 16, 1, 24),
+                                          (40, 128, 2049, 512)])
+def test_linear_heads_equals_linear_on_the_transposed_input(heads, hd, m, n):
+    """The out projection reading the head-major attention output equals the transpose + reshape + linear of the
+    reference (h3turbo/h3/model.py:226-228): bit-exact outputs, including the row-split quantiser for few rows."""
+    print(f"linear_heads heads={heads} hd={hd} m={m} n={n}", flush=True)
+    k = heads * hd
+    w = random_weight_gpu(n, k, seed=heads + hd)
+    g = torch.Generator(device=DEV).manual_seed(m)
+    big = (torch.randn(heads, m + 5, hd, generator=g, device=DEV) * 3).to(torch.bfloat16)
+    xh = big[:, 2:2 + m]  # a strided view: head stride (m + 5) * hd, token stride hd
+    want = ql.linear(xh.transpose(0, 1).reshape(m, k), w)
+    got = ql.linear_heads(xh, w)
+    assert torch.equal(got, want)
+    for mode in ("ck", "eager"):
+        assert torch.equal(ql.linear_heads(xh.contiguous(), w, quant_mode=mode),
+                           ql.linear(xh.transpose(0, 1).reshape(m, k), w, quant_mode=mode))

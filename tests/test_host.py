@@ -49,6 +49,22 @@ def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     assert lib.h3k_w4a8_linear_workspace(4, 8, 256) == 1024 + 256 + 2048
     # empty work is a no-op
     assert lib.h3k_rotate_quant(None, _lib.BF16, 0, 256, 256, 256, 0, None, 256, None, None) == 0
+    # split norm + rope: head_dim outside {32, 64, 128, 256}; overlapping head-major outputs
+    assert lib.h3k_qkv_split_norm_rope(None, 288, 4, 2, 48, None, None, None, None, 24, 24, 1e-5, None, None, None, 192,
+                                       None) == _lib.EINVAL
+    assert "head_dim" in lib.h3k_last_error().decode()
+    assert lib.h3k_qkv_split_norm_rope(None, 768, 4, 2, 128, None, None, None, None, 48, 48, 1e-5, None, None, None, 256,
+                                       None) == _lib.EINVAL
+    assert "head_stride" in lib.h3k_last_error().decode()
+    # head-major rotate+quant: only rotation 256 on 16-bit activations; head_dim a power of two
+    assert lib.h3k_rotate_quant_heads(None, _lib.BF16, 4, 512, 128, 128, 512, 64, 0, None, 512, None, None) == _lib.EINVAL
+    assert "rotation 256" in lib.h3k_last_error().decode()
+    assert lib.h3k_rotate_quant_heads(None, _lib.BF16, 4, 480, 96, 96, 384, 256, 0, None, 480, None, None) == _lib.EINVAL
+    assert "power of two" in lib.h3k_last_error().decode()
+    # fused RMSNorm + modulation: k a multiple of 8 up to 8192
+    assert lib.h3k_rms_modulate(None, 100, 4, 100, None, None, None, 100, None, 1e-5, None, 100, None) == _lib.EINVAL
+    assert "multiple of 8" in lib.h3k_last_error().decode()
+    assert lib.h3k_rms_modulate(None, 5120, 0, 5120, None, None, None, 5120, None, 1e-5, None, 5120, None) == 0
 
 
 def make_weight(n=40, k=512, group=16):
