@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--no-stream", action="store_true", help="skip the config-5 streamed 60-block stack")
     ap.add_argument("--sweep", action="store_true", help="add the config-3 GEMM sweep (16 shapes) to the line")
     ap.add_argument("--stream-blocks", type=int, default=60)
+    ap.add_argument("--no-h3t", action="store_true", help="skip the .h3t container measurement")
+    ap.add_argument("--h3t-blocks", type=int, default=8)
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="after the timed region, run 3 plain device-to-device copies of BYTES bytes: the reference "
@@ -237,6 +239,85 @@ def stream_measurement(dev, n_blocks: int):
             "h2d_GB_per_s": round(store.nbytes / t_copy / 1e9, 1), "overlap": round(overlap, 3),
             "streamed_equals_resident": bool(torch.equal(out_res, out_str)),
             "waits": st["waits"], "host_kinds": st["host_kinds"], "setup_s": round(t_setup, 1)}
+
+
+def h3t_measurement(dev, n_blocks: int):
+    """The .h3t container at the config-4 block shape: n_blocks random-init W4A8 blocks (GELU, g128 fp16 scales)
+    written as an .h3t file (the format of h3turbo/h3/store.py), loaded into pinned host memory
+    (HostBlockStore.from_h3t), then one streamed step (12090 + 512 tokens) with the blocks coming from the pinned
+    copy and from the file mapping (pageable pages copied through two pinned staging buffers).  Both outputs must equal
+    the all-resident output bit for bit."""
+    import json as _json
+    import tempfile
+
+    import torch
+
+    from h3turbo_amd import block as bk
+    from h3turbo_amd import h3t
+    from h3turbo_amd.blockstore import HostBlockStore, block_tensors
+    from h3turbo_amd.config import H3Config
+    from h3turbo_amd.stream import StreamingProvider
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    qjson = torch.tensor(list(_json.dumps({"format": "asym_w4a8_int8", "group_size": 128, "convrot_groupsize": 256},
+                                          separators=(",", ":")).encode()), dtype=torch.uint8)
+    tensors = {}
+    for i in range(n_blocks):
+        for name, t in block_tensors(_config4_block_weights(dev, g)).items():
+            tensors[f"blocks.{i}.{name}"] = t
+        for p in ("attn.qkv_proj", "attn.out_proj", "mlp.fc1", "mlp.fc2"):
+            tensors[f"blocks.{i}.{p}.comfy_quant"] = qjson
+    cfg = H3Config(hidden=5120, layers=n_blocks, heads=40, head_dim=128, ffn=13824, quant_group=128, quant_convrot=256)
+    tmpdir = tempfile.mkdtemp(prefix="h3t_bench_")
+    path = os.path.join(tmpdir, "stack.h3t")
+    try:
+        t0 = time.perf_counter()
+        h3t.write_h3t(path, cfg, tensors)
+        t_write = time.perf_counter() - t0
+        del tensors
+        nbytes = os.path.getsize(path)
+        with h3t.H3TFile(path) as f:
+            t0 = time.perf_counter()
+            pinned = HostBlockStore.from_h3t(f, pinned=True)
+            t_load = time.perf_counter() - t0
+            s, hidden = 12602, 5120
+            blk = bk.DiTBlock(bk.BlockConfig(hidden=hidden, heads=40, head_dim=128, ffn=13824, act="gelu"))
+            x0 = torch.randn(s, hidden, generator=g, device=dev).to(torch.bfloat16)
+            mods = [torch.randn(1, hidden, generator=g, device=dev) * 0.1 for _ in range(6)]
+            pos = torch.stack(torch.meshgrid(torch.arange(31), torch.arange(15), torch.arange(26), indexing="ij"), -1).reshape(-1, 3)
+            pos = torch.cat([pos + 1, torch.zeros(512, 3, dtype=pos.dtype)], 0)
+            rope = bk.rope_tables(pos, 1.0 / (10000.0 ** (torch.arange(16) / 16.0)), dev, torch.bfloat16)
+
+            def forward_time(p):
+                bk.run_blocks(blk, x0.clone(), p, n_blocks, lambda i, w: mods, [(0, s, 0)], rope)
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                out = bk.run_blocks(blk, x0.clone(), p, n_blocks, lambda i, w: mods, [(0, s, 0)], rope)
+                torch.cuda.synchronize()
+                return time.perf_counter() - t, out
+
+            with StreamingProvider(pinned, dev, resident=n_blocks) as p:
+                t_res, out_res = forward_time(p)
+            with StreamingProvider(pinned, dev, resident=0, ring=3, prefetch=2) as p:
+                t_pin, out_pin = forward_time(p)
+                kinds_pin = p.stats()["host_kinds"]
+            with StreamingProvider(f, dev, resident=0, ring=3, prefetch=2, pin_mode="stage") as p:
+                t_map, out_map = forward_time(p)
+                kinds_map = p.stats()["host_kinds"]
+        return {"config": f"{n_blocks} config-4 blocks (GELU, W4A8 g128 fp16 scales) in one .h3t file, S=12090+512",
+                "file_MB": round(nbytes / 1e6, 1), "block_MB": round(pinned.block_nbytes / 1e6, 1),
+                "write_s": round(t_write, 2), "load_pinned_s": round(t_load, 3),
+                "load_pinned_GB_per_s": round(pinned.nbytes / t_load / 1e9, 2),
+                "resident_forward_s": round(t_res, 4), "streamed_from_pinned_s": round(t_pin, 4),
+                "streamed_from_file_mapping_s": round(t_map, 4), "host_kinds_pinned": kinds_pin,
+                "host_kinds_mapping": kinds_map,
+                "outputs_equal_resident": bool(torch.equal(out_pin, out_res) and torch.equal(out_map, out_res))}
+    finally:
+        try:
+            os.remove(path)
+        except OSError:
+            pass
+        os.rmdir(tmpdir)
 
 
 def sweep_measurement(dev, steps: int):
@@ -443,6 +524,8 @@ def main() -> None:
         line["sweep"] = sweep_measurement(dev, 10)
     if not args.no_stream:
         line["stream"] = stream_measurement(dev, args.stream_blocks)
+    if not args.no_h3t:
+        line["h3t"] = h3t_measurement(dev, args.h3t_blocks)
     if args.copy_probe:
         src = torch.full((args.copy_probe,), 1, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

@@ -161,6 +161,21 @@ class HostBlockStore:
             st.write_block(i, first if i == 0 else block_tensors(b))
         return st
 
+    @classmethod
+    def from_h3t(cls, f, *, pinned: bool = False) -> "HostBlockStore":
+        """Copy every block of an open .h3t file (h3t.H3TFile) into a new store with the file's block layout, so the
+        blocks become DMA-ready host memory (pinned=True) instead of pageable file pages."""
+        from .h3t import torch_dtype
+
+        layout = BlockLayout([LayoutEntry(e.name, torch_dtype(e.dtype), tuple(e.shape), e.offset, e.nbytes)
+                              for e in f.block_layout])
+        if layout.nbytes != f.block_nbytes:
+            raise ValueError(f"{f.path}: block layout spans {layout.nbytes} bytes, the file's blocks are {f.block_nbytes}")
+        st = cls(layout, f.n_blocks, f.quant_group, f.quant_convrot, pinned=pinned)
+        for i in range(f.n_blocks):
+            np.copyto(st.block_bytes(i), f.block_bytes(i))
+        return st
+
     def _check(self, i: int) -> None:
         if not 0 <= i < self.n_blocks:
             raise IndexError(f"block {i} out of range [0, {self.n_blocks})")

@@ -3,8 +3,8 @@ H3Engine, h3turbo/h3/engine.py:29-132, restricted to the block stack).
 
 The reference engine also embeds the inputs, runs the token refiner, the output heads and an Euler sampler; those
 whole-model parts are not part of this build.  What it keeps is the part on the hot path: building the provider
-with the same options (from_store), running the block loop over it (blocks), and the introspection calls
-(linear_backend, stats, gpu_bytes, close).
+with the same options (from_store, from_h3t), running the block loop over it (blocks), and the introspection
+calls (linear_backend, stats, gpu_bytes, close).
 """
 from __future__ import annotations
 
@@ -14,6 +14,7 @@ import torch
 
 from . import qlinear
 from .block import BlockConfig, DiTBlock, Segment, run_blocks
+from .blockstore import HostBlockStore
 from .stream import StreamingProvider
 
 _GIB = 1 << 30
@@ -23,6 +24,34 @@ class H3Engine:
     def __init__(self, store, provider: StreamingProvider, block: DiTBlock, owns_store: bool = False):
         self.store, self.provider, self.block, self._owns_store = store, provider, block, owns_store
         self.cfg = block.cfg
+
+    @classmethod
+    def from_h3t(cls, path, device: Optional[str] = None, *, load_pinned: Optional[bool] = None, **kw) -> "H3Engine":
+        """Open an .h3t file and build an engine over its blocks (h3turbo/h3/engine.py:33-44).  The block config
+        comes from the file's H3Config (the H3 block: SwiGLU MLP).  load_pinned (default: on a GPU) first copies
+        every block into page-locked host memory, so the streamed blocks reach HBM as direct DMA transfers; with
+        False the engine streams from the file mapping through its staging buffers."""
+        from .h3t import H3TFile
+
+        f = H3TFile(path)
+        try:
+            c = f.cfg
+            if kw.get("block_config") is None:
+                kw["block_config"] = BlockConfig(hidden=c.hidden, heads=c.heads, head_dim=c.head_dim, ffn=c.ffn,
+                                                 act="swiglu", norm_eps=c.norm_eps, qk_norm_eps=c.qk_norm_eps,
+                                                 rope_freqs=c.rope_inv_freq_len)
+            dev = torch.device(device or ("cuda" if torch.cuda.is_available() else "cpu"))
+            if load_pinned is None:
+                load_pinned = dev.type == "cuda"
+            if load_pinned:
+                store = HostBlockStore.from_h3t(f, pinned=True)
+                f.close()
+            else:
+                store = f
+            return cls.from_store(store, str(dev), owns_store=True, **kw)
+        except BaseException:
+            f.close()
+            raise
 
     @classmethod
     def from_store(cls, store, device: Optional[str] = None, *, block_config: Optional[BlockConfig] = None,

@@ -323,9 +323,12 @@ def linear_heads(xh: torch.Tensor, w: W4A8Weight, *, out_dtype: Optional[torch.d
     if m == 0:
         return torch.empty(0, n, dtype=out_dtype, device=xh.device)
     _need_gpu(xh, "linear_heads")
-    if xh.dtype not in (torch.bfloat16, torch.float16):
-        raise ValueError(f"linear_heads takes bf16 or f16 activations, got {xh.dtype}")
-    if xh.stride(2) != 1 or xh.stride(1) < hd or (heads > 1 and xh.stride(0) < m * xh.stride(1)):
+    if (xh.dtype not in (torch.bfloat16, torch.float16) or w.convrot != 256 or hd < 16 or hd & (hd - 1)
+            or k % 256 or k > 256 * 128):
+        # no head-major kernel for this case: the transpose copy and the plain linear
+        return linear(xh.transpose(0, 1).reshape(m, k), w, out_dtype=out_dtype, quant_mode=quant_mode)
+    if (xh.stride(2) != 1 or xh.stride(1) < hd or (heads > 1 and xh.stride(0) < m * xh.stride(1))
+            or xh.data_ptr() % 16 or (2 * xh.stride(1)) % 16 or (heads > 1 and (2 * xh.stride(0)) % 16)):
         xh = xh.contiguous()
     ldx, hstride = xh.stride(1), (xh.stride(0) if heads > 1 else m * xh.stride(1))
     runner = _HipRunner(w, None, out_dtype, "a8", quant_mode)

@@ -107,3 +107,42 @@ def test_streamed_dit_stack_equals_the_resident_stack():
             for _ in range(2):  # the second forward starts from the cyclic prefetch of the first
                 outs.append(bk.run_blocks(blk, x.clone(), p, 8, lambda i, w: mods, [(0, 700, 0)], rope))
     assert all(torch.equal(o, outs[0]) for o in outs[1:])
+
+
+def test_engine_from_h3t_streams_the_file_blocks():
+    """A W4A8 .h3t file (the reference writer's golden file) through H3Engine.from_h3t: streamed from pinned host
+    memory, streamed from the file mapping, and run block by block from the file's own views all give the same
+    residual, bit for bit."""
+    import os
+
+    from h3turbo_amd import h3t
+    from h3turbo_amd.engine import H3Engine
+    from h3turbo_amd.types import BlockWeights, W4A8Weight
+
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "vectors", "h3t_tiny_quant.h3t")
+    cfg = bk.BlockConfig(hidden=64, heads=2, head_dim=32, ffn=48, act="swiglu", rope_freqs=4)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    s = 40
+    x0 = torch.randn(s, 64, generator=g, device=DEV).to(torch.bfloat16)
+    mods = [torch.randn(2, 64, generator=g, device=DEV) * 0.1 for _ in range(6)]
+    segs = [(0, 25, 0), (25, s, 1)]
+    ang = torch.rand(s, 12, generator=g, device=DEV) * 6
+    rope = (torch.cos(ang).to(torch.bfloat16), torch.sin(ang).to(torch.bfloat16))
+    outs = []
+    for kw in (dict(resident=0, ring=2), dict(load_pinned=False, resident=0, ring=2, pin=False), dict(resident="auto")):
+        with H3Engine.from_h3t(golden, "cuda", block_config=cfg, **kw) as eng:
+            assert eng.linear_backend() == "hip"
+            outs.append(eng.blocks(x0.clone(), lambda i, w: mods, segs, rope))
+    torch.cuda.synchronize()
+    blk = bk.DiTBlock(cfg)
+    x = x0.clone()
+    with h3t.H3TFile(golden) as f:
+        for i in range(f.n_blocks):
+            w = f.block_weights_cpu(i)
+            dev = lambda t: t.to(DEV) if isinstance(t, torch.Tensor) else (t.to(DEV) if isinstance(t, W4A8Weight) else t)  # noqa: E731
+            wd = BlockWeights(**{k: dev(getattr(w, k)) for k in ("qkv", "out", "fc1", "fc2", "norm1", "norm2", "q_norm",
+                                                                  "k_norm", "adaln_w", "adaln_b")})
+            x = blk(x, wd, mods, segs, rope)
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, x)
