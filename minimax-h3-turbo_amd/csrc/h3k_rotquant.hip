@@ -63,7 +63,9 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
                                                           int64_t ldx, int hshift, int64_t hstride,
                                                           int8_t* __restrict__ q, int64_t ldq, float* __restrict__ xs) {
   static_assert(WPR == 1 || WPR == 4, "one row per wavefront or one row per workgroup");
-  __shared__ __attribute__((aligned(16))) uint16_t s_in[4][4 * kInStride];
+  // The 16-bit input transpose and the fp64 mid transpose of a pass never overlap in time, so they share one
+  // buffer: 35 KiB per workgroup instead of 44 KiB lets four workgroups (4 waves per SIMD) share a CU.
+  static_assert(kInStride * 2 <= kMidStride * 8, "input transpose must fit the mid-transpose area");
   __shared__ __attribute__((aligned(16))) double s_mid[4][4 * kMidStride];
   __shared__ float s_amax[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     }
   }
 
-  uint16_t* tin = &s_in[wave][g * kInStride];
+  uint16_t* tin = reinterpret_cast<uint16_t*>(&s_mid[wave][g * kMidStride]);
   double* tmid = &s_mid[wave][g * kMidStride];
   uint32_t yb[NPASS][8];  // rounded rotation, two 16-bit values per word, contiguous elements l*16 ..
   float amax = 0.0f;
@@ -112,6 +114,7 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
 #pragma unroll
     for (int d2 = 0; d2 < 4; ++d2) h4(v[d2], v[d2 + 4], v[d2 + 8], v[d2 + 12]);
     // (3) transpose the fp64 mid-values back: lane l then holds elements 16*l + j, j = 0..15 (digits 0,1 local)
+    wave_lds_sync();  // the input reads above are done before the area is overwritten
 #pragma unroll
     for (int r = 0; r < 16; ++r) tmid[r * kMidRow + l] = v[r];
     wave_lds_sync();
