@@ -1,7 +1,8 @@
 // int4 codebook indices -> exact int8 grid (reference h3turbo/h3/qlinear.py:157-204):
 //   w8[n, k] = clamp(rint_half_even(f32(codebook[nib(n, k)]) * f32(s_rel[n, k / group])), -127, 127)
 // nib(n, 2j) is the LOW nibble of q[n, j]; a NaN product (NaN scale byte) decodes to 0 like the reference's
-// nan_to_num'd pair table.  HBM-bound: each thread turns 8 packed bytes into 16 levels (one 16-byte store).
+// nan_to_num'd pair table.  HBM-bound: each thread turns 8 packed bytes into 16 levels (one 16-byte store), or for
+// groups of 32 or more 32 levels through a 16-entry byte table per scale (decode_w4_lut_kernel).
 #include "h3k_common.hpp"
 
 namespace h3k {
@@ -56,9 +57,82 @@ __global__ __launch_bounds__(256) void decode_w4_kernel(const uint8_t* __restric
   *reinterpret_cast<uint4*>(w8 + row * ldw + c * 16) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
+// Groups of 32 or more: a thread owns 32 consecutive levels of one row (16 packed bytes in, 32 bytes out, so a
+// wavefront's loads and stores are contiguous) that share one scale.  The scale's 16 possible levels form a byte
+// table in 4 registers (byte c of word w = level(codebook[4w + c], s)); the SH lanes of a quad that share the
+// scale each compute 4/SH of its words and broadcast them with DPP quad permutes.  A nibble becomes its level
+// with byte permutes: one v_perm_b32 over entries 0-7, one over entries 8-15, and a third that picks between
+// them on the nibble's bit 3.  The levels are the same values the per-element path computes.
+__device__ __forceinline__ uint32_t lut_lookup(const uint32_t (&lut)[4], uint32_t sel, uint32_t b3) {
+  const uint32_t lo = __builtin_amdgcn_perm(lut[1], lut[0], sel);  // sel: nibble & 7 per byte
+  const uint32_t hi = __builtin_amdgcn_perm(lut[3], lut[2], sel);
+  return __builtin_amdgcn_perm(hi, lo, 0x03020100u | b3);  // b3: 4 in bytes whose nibble has bit 3 set
+}
+
+template <int SD, int SH>
+__global__ __launch_bounds__(256) void decode_w4_lut_kernel(const uint8_t* __restrict__ q, int64_t ldq,
+                                                            const void* __restrict__ s_rel, int64_t lds,
+                                                            const float* __restrict__ cb, int n, int k, int group,
+                                                            int8_t* __restrict__ w8, int64_t ldw) {
+  static_assert(SH == 1 || SH == 2 || SH == 4, "lanes sharing a scale");
+  const int chunks = k >> 5;  // a multiple of SH (host), so whole quads stay in one row and one scale group
+  const int t = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (t >= n * chunks) return;  // whole quads; n * chunks < 2^31 (host)
+  const int row = t / chunks;
+  const int c = t - row * chunks;
+  const u32x4 pk = *reinterpret_cast<const u32x4*>(q + static_cast<int64_t>(row) * ldq + c * 16);
+  const float s = load_scale<SD>(s_rel, static_cast<int64_t>(row) * lds + (c * 32) / group);
+  constexpr int NW = 4 / SH;
+  const int j = t & (SH - 1);
+  uint32_t mine[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int w = j * NW + i;
+    mine[i] = level(cb[4 * w], s) | (level(cb[4 * w + 1], s) << 8) | (level(cb[4 * w + 2], s) << 16) |
+              (level(cb[4 * w + 3], s) << 24);
+  }
+  uint32_t lut[4];
+  if constexpr (SH == 1) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) lut[w] = mine[w];
+  } else if constexpr (SH == 2) {  // quad_perm [0,0,2,2] / [1,1,3,3]
+    lut[0] = __builtin_amdgcn_mov_dpp(mine[0], 0xA0, 0xF, 0xF, false);
+    lut[1] = __builtin_amdgcn_mov_dpp(mine[1], 0xA0, 0xF, 0xF, false);
+    lut[2] = __builtin_amdgcn_mov_dpp(mine[0], 0xF5, 0xF, 0xF, false);
+    lut[3] = __builtin_amdgcn_mov_dpp(mine[1], 0xF5, 0xF, 0xF, false);
+  } else {  // quad_perm [w,w,w,w]
+    lut[0] = __builtin_amdgcn_mov_dpp(mine[0], 0x00, 0xF, 0xF, false);
+    lut[1] = __builtin_amdgcn_mov_dpp(mine[0], 0x55, 0xF, 0xF, false);
+    lut[2] = __builtin_amdgcn_mov_dpp(mine[0], 0xAA, 0xF, 0xF, false);
+    lut[3] = __builtin_amdgcn_mov_dpp(mine[0], 0xFF, 0xF, 0xF, false);
+  }
+  uint32_t o[8];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t dlo = lut_lookup(lut, pk[w] & 0x07070707u, (pk[w] >> 1) & 0x04040404u);  // even k: low nibbles
+    const uint32_t dhi = lut_lookup(lut, (pk[w] >> 4) & 0x07070707u, (pk[w] >> 5) & 0x04040404u);  // odd k
+    o[2 * w] = __builtin_amdgcn_perm(dhi, dlo, 0x05010400u);      // lo0 hi0 lo1 hi1
+    o[2 * w + 1] = __builtin_amdgcn_perm(dhi, dlo, 0x07030602u);  // lo2 hi2 lo3 hi3
+  }
+  int8_t* dst = w8 + static_cast<int64_t>(row) * ldw + c * 32;
+  *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+  *reinterpret_cast<u32x4*>(dst + 16) = u32x4{o[4], o[5], o[6], o[7]};
+}
+
 template <int SD>
 static void launch_decode(const void* q, int64_t ldq, const void* s_rel, int64_t lds, const float* cb, int64_t n, int k,
                           int group, int8_t* w8, int64_t ldw, hipStream_t st) {
+  const int sh = group % 128 == 0 ? 4 : (group % 64 == 0 ? 2 : 1);
+  if (group % 32 == 0 && n * (k / 32) < (int64_t(1) << 31) - 256 && aligned(q, 16) && ldq % 16 == 0) {
+    const dim3 g(static_cast<unsigned>((n * (k / 32) + 255) / 256));
+    const int nn = static_cast<int>(n);
+#define H3K_DL(SH)                                                                                                  \
+    hipLaunchKernelGGL((decode_w4_lut_kernel<SD, SH>), g, dim3(256), 0, st, static_cast<const uint8_t*>(q), ldq,   \
+                       s_rel, lds, cb, nn, k, group, w8, ldw)
+    if (sh == 4) H3K_DL(4); else if (sh == 2) H3K_DL(2); else H3K_DL(1);
+#undef H3K_DL
+    return;
+  }
   const int64_t threads = n * (k / 16);
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   if (group < 16)

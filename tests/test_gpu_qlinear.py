@@ -290,7 +290,7 @@ def test_degenerate_rows():
 
 
 # ---------------------------------------------------------------------------------------------- decode
-@pytest.mark.parametrize("group", [4, 8, 16, 32, 128])
+@pytest.mark.parametrize("group", [4, 8, 16, 32, 64, 128, 256])
 @pytest.mark.parametrize("s_kind", ["fp8", "f16", "bf16", "f32"])
 def test_decode_all_scale_kinds_and_groups(group, s_kind):
     n, k = 37, 512
@@ -317,6 +317,27 @@ def test_decode_ties_clamp_and_views_into_larger_buffers():
     sub = W4A8Weight(big[3:-2], torch.from_numpy(ss).view(torch.float8_e4m3fn).to(DEV), torch.from_numpy(s_ch).to(DEV),
                      torch.from_numpy(cbb).to(DEV), 16, 128)
     assert torch.equal(ql.decode_int8_grid(sub), full)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+@pytest.mark.parametrize("pad", [0, 8, 16])
+def test_decode_table_path_every_byte_nan_and_clamp_scales(group, pad):
+    """Groups of 32 or more decode through a per-scale byte table: every packed byte value, NaN / +-448 / zero /
+    negative fp8 scales, rows that are views with a 16-byte (table path) or 8-byte (per-element path) stride."""
+    n, k = 24, 1024
+    rng = np.random.default_rng(group + pad)
+    q = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    q[0] = np.arange(256, dtype=np.uint8).repeat(k // 512)
+    s = rng.integers(0, 256, (n, k // group), dtype=np.uint8)  # every e4m3fn byte: NaN 0x7F/0xFF, negatives
+    s[1], s[2], s[3], s[4] = 0x7F, 0x7E, 0xFE, 0x00  # NaN, 448, -448, 0
+    _, _, _, cb = gi.weight_fp8_g16(4, 64, seed=1)
+    want = ref.decode_int8_grid(q.view(np.int8), s, "fp8", cb, group)
+    big = torch.zeros(n, k // 2 + pad + 16, dtype=torch.int8)
+    big[:, pad:pad + k // 2] = torch.from_numpy(q.view(np.int8))
+    qd = big.to(DEV)[:, pad:pad + k // 2]
+    w = W4A8Weight(qd, torch.from_numpy(s).view(torch.float8_e4m3fn).to(DEV), torch.ones(n, device=DEV),
+                   torch.from_numpy(cb).to(DEV), group, 256)
+    assert np.array_equal(ql.decode_int8_grid(w).cpu().numpy(), want)
 
 
 # ---------------------------------------------------------------------------------------------- accuracy (a8 / a16)
