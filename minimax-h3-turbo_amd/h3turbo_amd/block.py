@@ -369,12 +369,14 @@ class DiTBlock:
 
 
 def _sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-    """Exact attention on the GPU's flash / memory-efficient kernels.  The unfused math backend is never used on
-    the GPU: it would materialise [heads, S, S] scores and run batched bf16 products on transposed operands."""
+    """Exact attention on the GPU's flash / memory-efficient kernels for 16-bit inputs.  The unfused math backend
+    never sees 16-bit inputs on the GPU (it would materialise [heads, S, S] scores and run batched 16-bit products
+    on transposed operands); fp32 inputs, which the flash kernels do not take, use it."""
     if q.is_cuda:
         from torch.nn.attention import SDPBackend, sdpa_kernel
 
-        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        fp32 = q.dtype == torch.float32
+        with sdpa_kernel([SDPBackend.MATH] if fp32 else [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             return F.scaled_dot_product_attention(q, k, v)
     return F.scaled_dot_product_attention(q, k, v)
 

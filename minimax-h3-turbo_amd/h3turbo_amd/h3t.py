@@ -28,7 +28,7 @@ import numpy as np
 import torch
 
 from .config import H3Config
-from .types import BlockWeights, W4A8Weight, Weight
+from .types import BlockWeights, GlobalWeights, W4A8Weight, Weight
 
 if sys.byteorder != "little":  # pragma: no cover - safetensors data is little-endian
     raise ImportError(".h3t files are little-endian; big-endian hosts are unsupported")
@@ -187,6 +187,13 @@ def build_block_weights(get: Callable[[str], torch.Tensor], has: Callable[[str],
                         adaln_b=get("adaln_proj.linear.bias") if mod else None)
 
 
+_GLOBALS_NEEDED = ("video_patch_proj.weight", "video_patch_proj.bias", "audio_patch_proj.weight",
+                   "audio_patch_proj.bias", "condition_proj.weight", "condition_proj.bias", "rope.inv_freq",
+                   "final_layer.norm.weight", "final_layer.adaln_proj.linear.weight",
+                   "final_layer.adaln_proj.linear.bias", "final_layer.video_out.weight", "final_layer.video_out.bias",
+                   "final_layer.audio_out.weight", "final_layer.audio_out.bias")
+
+
 # ------------------------------------------------------------------------------------------------ reader
 class H3TFile:
     """A read-only memory-mapped .h3t file (h3turbo/h3/store.py:182-400).  Every accessor returns a zero-copy view of
@@ -328,6 +335,45 @@ class H3TFile:
 
     def block_weights_cpu(self, i: int) -> BlockWeights:
         return self.block_weights_from(self.block_tensor(i))
+
+    def load_globals(self, device="cpu", *, refiner_device=None) -> GlobalWeights:
+        """GlobalWeights on `device`, the token refiner on `refiner_device` (default: the same) (reference
+        h3turbo/h3/store.py:329-365).  On the CPU the globals are copies and the refiner stays zero-copy views of
+        the mapping; refiner_device="cpu" keeps the refiner out of HBM until the text is encoded."""
+        dev = torch.device(device)
+        rdev = torch.device(refiner_device) if refiner_device is not None else dev
+
+        def get(name: str, d: torch.device = dev, view: bool = False) -> torch.Tensor:
+            t = self.tensor(name)
+            if d.type != "cpu":
+                return t.to(d)
+            return t if view else t.clone()
+
+        missing = [n for n in _GLOBALS_NEEDED if n not in self._info]
+        if missing:
+            raise H3TError(f"{self.path}: missing global tensors {missing}")
+        refiner = []
+        for j in range(self.cfg.refiner_layers):
+            pre = f"token_refiner.blocks.{j}."
+            refiner.append(build_block_weights(lambda r, pre=pre: get(pre + r, rdev, True),
+                                               lambda r, pre=pre: pre + r in self._info, self.quant_group,
+                                               self.quant_convrot, adaln=False))
+        fnorm = "token_refiner.final_norm.weight"
+        return GlobalWeights(
+            video_patch_w=get("video_patch_proj.weight"), video_patch_b=get("video_patch_proj.bias"),
+            audio_patch_w=get("audio_patch_proj.weight"), audio_patch_b=get("audio_patch_proj.bias"),
+            condition_w=get("condition_proj.weight"), condition_b=get("condition_proj.bias"),
+            adaln_t_table=get("adaln_t_table") if "adaln_t_table" in self._info else None,
+            rope_inv_freq=get("rope.inv_freq"), final_norm=get("final_layer.norm.weight"),
+            final_adaln_w=get("final_layer.adaln_proj.linear.weight"),
+            final_adaln_b=get("final_layer.adaln_proj.linear.bias"),
+            video_out_w=get("final_layer.video_out.weight"), video_out_b=get("final_layer.video_out.bias"),
+            audio_out_w=get("final_layer.audio_out.weight"), audio_out_b=get("final_layer.audio_out.bias"),
+            refiner=refiner, refiner_final_norm=get(fnorm, rdev, True) if fnorm in self._info else None)
+
+    def has_globals(self) -> bool:
+        """Whether the file holds every global tensor the whole-model forward needs."""
+        return all(n in self._info for n in _GLOBALS_NEEDED)
 
     def globals_nbytes(self, refiner: bool = True) -> int:
         """Bytes of the tensors outside the blocks (the token refiner optional)."""

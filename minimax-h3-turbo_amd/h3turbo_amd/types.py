@@ -5,8 +5,8 @@ reference plug in unchanged.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
-from typing import Optional, Protocol, Union
+from dataclasses import dataclass, field
+from typing import List, Optional, Protocol, Union
 
 import torch
 
@@ -69,6 +69,30 @@ class BlockWeights:
     k_norm: torch.Tensor  # [head_dim]
     adaln_w: Optional[torch.Tensor] = None
     adaln_b: Optional[torch.Tensor] = None
+
+
+@dataclass
+class GlobalWeights:
+    """The tensors outside the blocks (small, kept resident) plus the token refiner (reference
+    h3turbo/h3/types.py:70-90)."""
+
+    video_patch_w: torch.Tensor  # [hidden, video_patch_dim] (fp32 in the checkpoint)
+    video_patch_b: torch.Tensor
+    audio_patch_w: torch.Tensor  # [hidden, audio_channels]
+    audio_patch_b: torch.Tensor
+    condition_w: torch.Tensor  # [hidden, text_dim]
+    condition_b: torch.Tensor
+    adaln_t_table: Optional[torch.Tensor]  # [curve_grid, t_dim] fp32 (curve-form checkpoints)
+    rope_inv_freq: torch.Tensor  # [rope_inv_freq_len] fp32
+    final_norm: torch.Tensor  # [hidden]
+    final_adaln_w: torch.Tensor  # [2 * hidden, t_dim]
+    final_adaln_b: torch.Tensor  # [2 * hidden]
+    video_out_w: torch.Tensor  # [video_patch_dim * head_bank, hidden]
+    video_out_b: torch.Tensor
+    audio_out_w: torch.Tensor  # [audio_channels * head_bank, hidden]
+    audio_out_b: torch.Tensor
+    refiner: List[BlockWeights] = field(default_factory=list)  # token refiner blocks (no AdaLN)
+    refiner_final_norm: Optional[torch.Tensor] = None
 
 
 class BlockProvider(Protocol):
