@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="add the config-3 GEMM sweep (16 shapes) to the line")
     ap.add_argument("--stream-blocks", type=int, default=60)
     ap.add_argument("--no-h3t", action="store_true", help="skip the .h3t container measurement")
+    ap.add_argument("--no-model", action="store_true", help="skip the whole-model forward at the H3 shape")
+    ap.add_argument("--model-layers", type=int, default=50)
     ap.add_argument("--h3t-blocks", type=int, default=8)
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -176,6 +178,83 @@ def _config4_block_weights(dev, g):
     ones = lambda d: (1.0 + 0.1 * torch.randn(d, generator=g, device=dev))  # noqa: E731
     return BlockWeights(qkv=lin(15360, 5120), out=lin(5120, 5120), fc1=lin(13824, 5120), fc2=lin(5120, 13824),
                         norm1=ones(5120), norm2=ones(5120), q_norm=ones(128), k_norm=ones(128))
+
+
+def model_measurement(dev, layers: int, steps: int):
+    """The whole H3 model forward (one sampler step) at the real H3 shape: hidden 5376, 56 x 128 heads, SwiGLU FFN
+    14336, `layers` DiT blocks resident in HBM with W4A8 linears in the checkpoint's format (fp8 e4m3 group-16
+    scales, rotation 256, random codes), a dense bf16 2-block token refiner, S = 112 text + 400 audio + 12090 video
+    tokens (latent 31 x 30 x 52), bf16 compute.  Times encode_text once and the forward (embedding, every block,
+    final layer) over `steps` calls after one warmup."""
+    import torch
+
+    from h3turbo_amd.block import ResidentProvider
+    from h3turbo_amd.config import H3Config
+    from h3turbo_amd.model import H3Model
+    from h3turbo_amd.types import BlockWeights, GlobalWeights, W4A8Weight
+
+    cfg = H3Config(layers=layers)
+    hid, inner, ffn, td = cfg.hidden, cfg.inner, cfg.ffn, cfg.t_dim
+    g = torch.Generator(device=dev).manual_seed(7)
+    f32, bf = torch.float32, torch.bfloat16
+
+    def rn(*shape, std=1.0, dtype=f32):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(dtype)
+
+    cb = torch.linspace(-1, 1, 16, device=dev)
+
+    def w4(n, k):
+        q = torch.randint(-128, 128, (n, k // 2), generator=g, device=dev, dtype=torch.int8)
+        s_rel = (20 + 100 * torch.rand(n, k // 16, generator=g, device=dev)).to(torch.float8_e4m3fn)
+        s_ch = torch.full((n,), k ** -0.5 / 40.0, device=dev)
+        return W4A8Weight(q, s_rel, s_ch, cb, group_size=16, convrot=256)
+
+    def ones(d):
+        return (1.0 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf)
+
+    blocks = [BlockWeights(qkv=w4(3 * inner, hid), out=w4(hid, inner), fc1=w4(2 * ffn, hid), fc2=w4(hid, ffn),
+                           norm1=ones(hid), norm2=ones(hid), q_norm=ones(cfg.head_dim), k_norm=ones(cfg.head_dim),
+                           adaln_w=rn(18 * hid, td, std=0.05), adaln_b=rn(18 * hid, std=0.05)) for _ in range(layers)]
+    refiner = [BlockWeights(qkv=rn(3 * inner, hid, std=hid ** -0.5, dtype=bf), out=rn(hid, inner, std=inner ** -0.5, dtype=bf),
+                            fc1=rn(2 * ffn, hid, std=hid ** -0.5, dtype=bf), fc2=rn(hid, ffn, std=ffn ** -0.5, dtype=bf),
+                            norm1=ones(hid), norm2=ones(hid), q_norm=ones(cfg.head_dim), k_norm=ones(cfg.head_dim))
+               for _ in range(cfg.refiner_layers)]
+    grid = torch.linspace(0, 1, cfg.curve_grid, device=dev)
+    pd, ac = cfg.video_patch_dim, cfg.audio_channels
+    glob = GlobalWeights(
+        video_patch_w=rn(hid, pd, std=0.1), video_patch_b=rn(hid, std=0.1), audio_patch_w=rn(hid, ac, std=0.1),
+        audio_patch_b=rn(hid, std=0.1), condition_w=rn(hid, cfg.text_dim, std=cfg.text_dim ** -0.5, dtype=bf),
+        condition_b=rn(hid, std=0.1, dtype=bf),
+        adaln_t_table=torch.stack([torch.sin(6.28 * (1 + j) * grid + j) * 0.5 for j in range(td)], 1),
+        rope_inv_freq=1.0 / (10000.0 ** (torch.arange(cfg.rope_inv_freq_len, device=dev) / cfg.rope_inv_freq_len)),
+        final_norm=ones(hid), final_adaln_w=rn(2 * hid, td, std=0.05), final_adaln_b=rn(2 * hid, std=0.05),
+        video_out_w=rn(pd, hid, std=hid ** -0.5), video_out_b=rn(pd, std=0.1), audio_out_w=rn(ac, hid, std=hid ** -0.5),
+        audio_out_b=rn(ac, std=0.1), refiner=refiner, refiner_final_norm=ones(hid))
+    m = H3Model(cfg, glob, ResidentProvider(blocks), device=dev, dtype=bf)
+    video = rn(1, cfg.video_channels, 31, 30, 52, dtype=bf)
+    audio = rn(1, ac, 2, 200, dtype=bf)
+    text = rn(1, 112, cfg.text_dim, dtype=bf)
+    weights_gb = sum(w.nbytes for b in blocks for w in (b.qkv, b.out, b.fc1, b.fc2)) / 1e9
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    refined = m.encode_text(text)
+    torch.cuda.synchronize()
+    t_text = time.perf_counter() - t0
+    out = m.forward([video, audio], 0.7, None, refined_text=refined)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = m.forward([video, audio], 0.7, None, refined_text=refined)
+    torch.cuda.synchronize()
+    t_fwd = (time.perf_counter() - t0) / steps
+    ok = bool(torch.isfinite(out[0]).all() and torch.isfinite(out[1]).all())
+    del blocks, glob, m, out
+    torch.cuda.empty_cache()
+    return {"config": f"H3 shape: hidden 5376, {layers} blocks, 56x128 heads, SwiGLU FFN 14336, W4A8 fp8 g16 (resident), "
+                      "dense bf16 refiner x2, S=12602 (text 112 + audio 2x200 + video 31x15x26), bf16",
+            "blocks_GB": round(weights_gb, 2), "encode_text_ms": round(t_text * 1e3, 2),
+            "forward_s": round(t_fwd, 4), "ms_per_block": round(t_fwd * 1e3 / layers, 3), "steps": steps,
+            "outputs_finite": ok}
 
 
 def stream_measurement(dev, n_blocks: int):
@@ -522,6 +601,8 @@ def main() -> None:
         line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))
     if args.sweep:
         line["sweep"] = sweep_measurement(dev, 10)
+    if not args.no_model:
+        line["model"] = model_measurement(dev, args.model_layers, 2)
     if not args.no_stream:
         line["stream"] = stream_measurement(dev, args.stream_blocks)
     if not args.no_h3t:

@@ -91,6 +91,10 @@ class H3Engine:
         engine a budget); reserve_gb is still kept for activations.  glob / model_cfg: the model's global weights and
         H3Config; by default taken from the store when it has them (an H3TFile).  model_kw go to H3Model."""
         dev = torch.device(device or ("cuda" if torch.cuda.is_available() else "cpu"))
+        c = getattr(store, "cfg", None)
+        if block_config is None and c is not None:  # the store's H3 block (SwiGLU MLP)
+            block_config = BlockConfig(hidden=c.hidden, heads=c.heads, head_dim=c.head_dim, ffn=c.ffn, act="swiglu",
+                                       norm_eps=c.norm_eps, qk_norm_eps=c.qk_norm_eps, rope_freqs=c.rope_inv_freq_len)
         cfg = block_config or BlockConfig()
         if whole_model and glob is None and hasattr(store, "has_globals") and store.has_globals():
             glob = store.load_globals(dev, refiner_device=dev if refiner_on_gpu else "cpu")

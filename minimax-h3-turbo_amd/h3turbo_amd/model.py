@@ -73,7 +73,7 @@ class H3Model:
                 raise ValueError(f"{name} must be >= 1")
         self.cfg, self.provider, self.device, self.dtype = cfg, provider, torch.device(device), dtype
         self.backend, self.precision, self.attn_impl = backend, precision, attn_impl
-        self.mlp_chunk, self.attn_chunk, self.rope_chunk = mlp_chunk, attn_chunk, rope_chunk
+        self.rope_chunk = rope_chunk
         self.rope_dtype = rope_dtype or dtype
         self.rope_impl = resolve_rope_impl(rope_impl, device, dtype, self.rope_dtype)
         self.glob = glob
@@ -106,6 +106,27 @@ class H3Model:
         self.head_bank = self.vow.shape[0] // pd
         self._layouts: Dict[tuple, PackedLayout] = {}
         self._rope: Optional[tuple] = None
+
+    @property
+    def mlp_chunk(self) -> Optional[int]:
+        """Tokens per MLP pass of the blocks (None: all); settable between forwards."""
+        return self.block.mlp_chunk
+
+    @mlp_chunk.setter
+    def mlp_chunk(self, v: Optional[int]) -> None:
+        if v is not None and v < 1:
+            raise ValueError("mlp_chunk must be >= 1")
+        self.block.mlp_chunk = v
+
+    @property
+    def attn_chunk(self) -> Optional[int]:
+        return self.block.attn_chunk
+
+    @attn_chunk.setter
+    def attn_chunk(self, v: Optional[int]) -> None:
+        if v is not None and v < 1:
+            raise ValueError("attn_chunk must be >= 1")
+        self.block.attn_chunk = v
 
     # -------------------------------------------------------------------------------------------- primitives
     def _island(self, t: torch.Tensor) -> torch.Tensor:

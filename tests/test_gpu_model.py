@@ -118,3 +118,37 @@ def test_streamed_engine_equals_resident_and_samples(tmp_path):
     torch.cuda.synchronize()
     for o in outs[1:]:
         assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1])
+
+
+def test_comfy_dit_streams_parks_and_shrinks_on_the_gpu(tmp_path):
+    """The host-application stand-in over a W4A8 .h3t: one resident block and the rest streamed through the ring give
+    the all-resident velocity bit for bit, before and after parking (no device memory) and shrinking."""
+    from h3turbo_amd.comfy_dit import H3TurboDiT, TorchMemoryHost
+    from h3turbo_amd.h3t import write_h3t
+
+    sd, _ = w4a8_case(50)
+    path = tmp_path / "w4.h3t"
+    write_h3t(path, CFG4, sd)
+    video, audio, text = mc.inputs(CFG4, 51)
+    x = [video.bfloat16().to(DEV), audio.bfloat16().to(DEV)]
+    ts = torch.tensor([620.0], device=DEV)
+    full = H3TurboDiT(str(path), host=TorchMemoryHost(DEV))
+    part = H3TurboDiT(str(path), resident_blocks=1, host=TorchMemoryHost(DEV))
+    try:
+        refined = full.preprocess_text_embeds(text.to(DEV))
+        want = full.forward(x, ts, refined)
+        assert full.engine.provider.stats()["resident"] == CFG4.layers
+        got = part.forward(x, ts, part.preprocess_text_embeds(text.to(DEV)))
+        st = part.engine.provider.stats()
+        assert st["resident"] == 1 and st["streamed"] == CFG4.layers - 1
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+        blk = part.store.block_nbytes
+        assert part.unload() > 0 and part.engine.provider.device_bytes() == 0
+        again = part.forward(x, ts, refined)
+        assert torch.equal(again[0], want[0])
+        assert part.shrink(blk) >= blk
+        assert torch.equal(part.forward(x, ts, refined)[0], want[0])
+        torch.cuda.synchronize()
+    finally:
+        part.close()
+        full.close()
