@@ -46,6 +46,7 @@ def parse():
     ap.add_argument("--stream-blocks", type=int, default=60)
     ap.add_argument("--no-h3t", action="store_true", help="skip the .h3t container measurement")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model forward at the H3 shape")
+    ap.add_argument("--no-few-rows", action="store_true", help="skip the small-M (16-128 rows) W4A8 GEMM measurement")
     ap.add_argument("--model-layers", type=int, default=50)
     ap.add_argument("--h3t-blocks", type=int, default=8)
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the CPU baseline sample")
@@ -453,6 +454,77 @@ def sweep_measurement(dev, steps: int):
     return rows
 
 
+def few_rows_measurement(dev, steps: int):
+    """Small-M W4A8 GEMMs against HBM: the BASELINE weight shape (N=13824, K=5120) with the BASELINE recipe (group
+    128, fp16 scales) and the checkpoint format (group 16, fp8 scales), M in {16, 64, 128}.  The fused few-row GEMM
+    (h3k_gemm_w4a8: int4 decoded in registers; zero-fill, GEMM and epilogue launches when it splits K) against the
+    decode + int8 GEMM pair it replaces.  HBM figure = algorithmic bytes (packed weight + scales + int8 activations
+    + xs + s_ch + bf16 out) / time of the fused call, HIP events on the launch stream."""
+    import torch
+
+    from h3turbo_amd import _lib
+    from h3turbo_amd import qlinear as ql
+    from h3turbo_amd.types import W4A8Weight
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    n, k = 13824, 5120
+    rows = []
+
+    def timed(fn):
+        for _ in range(3):
+            _lib.check(fn(), "few rows")
+        evs = []
+        for _ in range(steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            _lib.check(fn(), "few rows")
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in evs) / steps
+
+    for fmt in ("g128_f16", "g16_fp8"):
+        if fmt == "g128_f16":
+            q, s_rel, s_ch, cb = synth_weight(n, k, dev)
+            w = W4A8Weight(q, s_rel, s_ch, cb, group_size=128, convrot=256)
+        else:
+            g = torch.Generator(device=dev).manual_seed(5)
+            q = torch.randint(-128, 128, (n, k // 2), generator=g, device=dev, dtype=torch.int8)
+            s8 = (20 + 100 * torch.rand(n, k // 16, generator=g, device=dev)).to(torch.float8_e4m3fn)
+            w = W4A8Weight(q, s8, torch.full((n,), 1e-3, device=dev), torch.linspace(-1, 1, 16, device=dev), 16, 256)
+        dw = ql._DevWeight(w)
+        grp = w.group_size
+        sbytes = dw.s.numel() * dw.s.element_size()
+        w8 = torch.empty(n, k, dtype=torch.int8, device=dev)
+        for m in (16, 64, 128):
+            g = torch.Generator(device=dev).manual_seed(m)
+            xq = torch.randint(-127, 128, (m, k), generator=g, device=dev, dtype=torch.int8)
+            xs = torch.rand(m, 1, generator=g, device=dev) * 1e-3
+            out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            out2 = torch.empty_like(out)
+            nb = lib.h3k_gemm_w4a8_workspace(m, n, k)
+            ws = torch.empty(max(1, nb // 4), dtype=torch.int32, device=dev)
+            fused = lambda: lib.h3k_gemm_w4a8(xq.data_ptr(), k, xs.data_ptr(), dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(),  # noqa: E731
+                                               dw.scode, dw.lds, dw.cb.data_ptr(), grp, dw.s_ch.data_ptr(), None, m, n, k,
+                                               0, out.data_ptr(), _lib.BF16, n, ws.data_ptr(), None, sp)
+            dec = lambda: lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds,  # noqa: E731
+                                            dw.cb.data_ptr(), n, k, grp, w8.data_ptr(), k, sp)
+            gemm = lambda: lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, dw.s_ch.data_ptr(),  # noqa: E731
+                                             None, m, n, k, 0, out2.data_ptr(), _lib.BF16, n, None, sp)
+            t_f, t_d, t_g = timed(fused), timed(dec), timed(gemm)
+            same = bool(torch.equal(out, out2))
+            alg = n * k // 2 + sbytes + m * k + 4 * m + 4 * n + 2 * m * n
+            gbs = alg / (t_f * 1e-3) / 1e9
+            rows.append({"weight": fmt, "m": m, "fused_ms": round(t_f, 4), "fused_GB/s": round(gbs, 1),
+                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "decode_plus_gemm_ms": round(t_d + t_g, 4),
+                         "speedup": round((t_d + t_g) / t_f, 2), "outputs_equal": same})
+            del xq, xs, out, out2, ws
+        del dw, w8, w
+    return {"config": "N=13824 K=5120 (BASELINE weight), bf16 out, ck epilogue", "rows": rows}
+
+
 def cpu_baseline(m: int, k: int, n: int, rows: int):
     """Time the CPU oracle (restatement of the reference's torch CPU backend) on `rows` rows of the workload plus
     one per-call weight decode, and scale to M rows: TOPS = 2MNK / (t_decode + t_rows * M / rows)."""
@@ -601,6 +673,8 @@ def main() -> None:
         line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))
     if args.sweep:
         line["sweep"] = sweep_measurement(dev, 10)
+    if not args.no_few_rows:
+        line["few_rows"] = few_rows_measurement(dev, 20)
     if not args.no_model:
         line["model"] = model_measurement(dev, args.model_layers, 2)
     if not args.no_stream:

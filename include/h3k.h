@@ -85,7 +85,26 @@ int h3k_gemm_a8w8(const int8_t* a, int64_t lda, const float* xs, const int8_t* w
                   int32_t* acc_out, void* stream);
 
 /*
- * The whole W4A8 ConvRot linear: rotate+quantise x, decode the weight, GEMM + epilogue.
+ * W4A8 GEMM for few token rows (m <= 128): the int4 weight is decoded in registers into the int8 MFMA operands,
+ * so the int8 grid is never written; exact int32 accumulators and the epilogue of h3k_gemm_a8w8.
+ * Replaces, fused, h3turbo/h3/qlinear.py:157-204 (decode_int8_grid), :236-254 (_int8_mm) and :396-405 (_a8
+ * epilogue) for the calls with few rows.
+ *   a [m, k] int8 (lda bytes, 16-byte aligned), xs [m] float32
+ *   q packed [n, k/2] (ldq bytes, 16-byte aligned), s_rel [n, k/group] of s_dtype (lds elements), codebook [16]
+ *   group 16, 32 or a multiple of 64; k a multiple of 64
+ *   workspace: int32 scratch of h3k_gemm_w4a8_workspace(m, n, k) bytes (16-byte aligned; NULL when that is 0),
+ *   used when the call splits K; contents on entry are ignored
+ *   acc_out optional int32 [m, n] copy of the exact accumulators (NULL to skip)
+ */
+int64_t h3k_gemm_w4a8_workspace(int64_t m, int64_t n, int64_t k);
+int h3k_gemm_w4a8(const int8_t* a, int64_t lda, const float* xs, const void* q, int64_t ldq, const void* s_rel,
+                  int s_dtype, int64_t lds, const float* codebook, int group, const float* s_ch, const void* bias,
+                  int64_t m, int64_t n, int64_t k, int mode, void* out, int out_dtype, int64_t ldo, int32_t* workspace,
+                  int32_t* acc_out, void* stream);
+
+/*
+ * The whole W4A8 ConvRot linear: rotate+quantise x, decode the weight, GEMM + epilogue (m <= 128 with k a multiple
+ * of 64: the fused few-row GEMM, no decode pass).
  * Fills the slot of comfy_kitchen's w4a8_int8_linear call, h3turbo/h3/qlinear.py:427-429 (_run_ck).
  * workspace: device scratch of at least h3k_w4a8_linear_workspace(m, n, k) bytes, 256-byte aligned.
  */

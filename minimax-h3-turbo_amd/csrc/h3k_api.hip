@@ -44,10 +44,22 @@ extern "C" int h3k_version(void) { return 1; }
 
 extern "C" const char* h3k_last_error(void) { return g_last_error.c_str(); }
 
+// The weight region holds the decoded int8 grid, or for the fused few-row GEMM its split-K accumulators.
+static size_t weight_region(int64_t m, int64_t n, int64_t k) {
+  const size_t grid = static_cast<size_t>(n) * k;
+  const size_t acc = static_cast<size_t>(h3k_gemm_w4a8_workspace(m, n, k));
+  return grid > acc ? grid : acc;
+}
+
+static bool fused_few_rows(int64_t m, int64_t k, int group, const void* q, int64_t ldq) {
+  return m <= 128 && k % 64 == 0 && (group == 16 || group == 32 || (group > 0 && group % 64 == 0)) && k % group == 0 &&
+         aligned(q, 16) && ldq % 16 == 0;
+}
+
 extern "C" size_t h3k_w4a8_linear_workspace(int64_t m, int64_t n, int64_t k) {
   if (m < 0 || n < 0 || k < 0) return 0;
   return round_up(static_cast<size_t>(m) * k, 256) + round_up(static_cast<size_t>(m) * 4, 256) +
-         round_up(static_cast<size_t>(n) * k, 256);
+         round_up(weight_region(m, n, k), 256);
 }
 
 extern "C" int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* q,
@@ -66,6 +78,9 @@ extern "C" int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k,
   int8_t* w8 = reinterpret_cast<int8_t*>(ws + round_up(static_cast<size_t>(m) * k, 256) + round_up(static_cast<size_t>(m) * 4, 256));
   int rc = h3k_rotate_quant(x, x_dtype, m, k, ldx, rot, mode, aq, k, xs, stream);
   if (rc) return rc;
+  if (fused_few_rows(m, k, group, q, ldq))  // int4 decoded in registers: no int8 grid
+    return h3k_gemm_w4a8(aq, k, xs, q, ldq, s_rel, s_dtype, lds, codebook, group, s_ch, bias, m, n, k, mode, out,
+                         out_dtype, ldo, reinterpret_cast<int32_t*>(w8), nullptr, stream);
   rc = h3k_decode_w4(q, ldq, s_rel, s_dtype, lds, codebook, n, k, group, w8, k, stream);
   if (rc) return rc;
   return gemm_a8w8_launch(aq, k, xs, w8, k, s_ch, bias, m, n, k, mode, out, out_dtype, ldo, nullptr,

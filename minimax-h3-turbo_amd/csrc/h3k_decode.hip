@@ -3,24 +3,9 @@
 // nib(n, 2j) is the LOW nibble of q[n, j]; a NaN product (NaN scale byte) decodes to 0 like the reference's
 // nan_to_num'd pair table.  HBM-bound: each thread turns 8 packed bytes into 16 levels (one 16-byte store), or for
 // groups of 32 or more 32 levels through a 16-entry byte table per scale (decode_w4_lut_kernel).
-#include "h3k_common.hpp"
+#include "h3k_w4.hpp"
 
 namespace h3k {
-
-template <int SD>
-__device__ __forceinline__ float load_scale(const void* s, int64_t idx) {
-  if (SD == H3K_FP8E4M3) return fp8e4m3fn_to_f32(static_cast<const uint8_t*>(s)[idx]);
-  if (SD == H3K_F16) return f16_to_f32(static_cast<const uint16_t*>(s)[idx]);
-  if (SD == H3K_BF16) return bf16_to_f32(static_cast<const uint16_t*>(s)[idx]);
-  return static_cast<const float*>(s)[idx];
-}
-
-__device__ __forceinline__ uint32_t level(float cbv, float s) {
-  float p = cbv * s;
-  if (p != p) p = 0.0f;
-  p = __builtin_amdgcn_fmed3f(__builtin_rintf(p), -127.0f, 127.0f);
-  return static_cast<uint32_t>(static_cast<int>(p)) & 0xFFu;
-}
 
 template <int SD, bool SMALL_GROUP>
 __global__ __launch_bounds__(256) void decode_w4_kernel(const uint8_t* __restrict__ q, int64_t ldq,
@@ -63,12 +48,6 @@ __global__ __launch_bounds__(256) void decode_w4_kernel(const uint8_t* __restric
 // scale each compute 4/SH of its words and broadcast them with DPP quad permutes.  A nibble becomes its level
 // with byte permutes: one v_perm_b32 over entries 0-7, one over entries 8-15, and a third that picks between
 // them on the nibble's bit 3.  The levels are the same values the per-element path computes.
-__device__ __forceinline__ uint32_t lut_lookup(const uint32_t (&lut)[4], uint32_t sel, uint32_t b3) {
-  const uint32_t lo = __builtin_amdgcn_perm(lut[1], lut[0], sel);  // sel: nibble & 7 per byte
-  const uint32_t hi = __builtin_amdgcn_perm(lut[3], lut[2], sel);
-  return __builtin_amdgcn_perm(hi, lo, 0x03020100u | b3);  // b3: 4 in bytes whose nibble has bit 3 set
-}
-
 template <int SD, int SH>
 __global__ __launch_bounds__(256) void decode_w4_lut_kernel(const uint8_t* __restrict__ q, int64_t ldq,
                                                             const void* __restrict__ s_rel, int64_t lds,

@@ -236,9 +236,14 @@ def _swiglu(x: torch.Tensor) -> torch.Tensor:
     return F.silu(gate).mul_(up)
 
 
+FEW_ROWS = 128  # token chunks up to this many rows take the fused int4 GEMM (h3k_gemm_w4a8)
+
+
 class _HipRunner:
-    """W4A8 forward for one weight on the GPU: the weight's int8 grid is decoded once per call, then each token
-    chunk runs rotate+quantise and the int8 MFMA GEMM with the fused epilogue into its `out` slice."""
+    """W4A8 forward for one weight on the GPU.  Each token chunk runs rotate+quantise, then either the fused
+    few-row GEMM that decodes the int4 weight in registers (chunks of at most FEW_ROWS rows), or the int8 MFMA GEMM
+    over the weight's int8 grid, decoded once per call when first needed.  Both end in the fused epilogue written
+    into the chunk's `out` slice."""
 
     def __init__(self, w: W4A8Weight, bias: Optional[torch.Tensor], out_dtype: torch.dtype, precision: str, mode: str):
         self.w, self.out_dtype, self.precision, self.mode = w, out_dtype, precision, mode
@@ -246,8 +251,17 @@ class _HipRunner:
         self.n, self.k = self.dw.n, self.dw.k
         self.ocode = _lib.act_code(out_dtype)
         self.bias = None if bias is None else bias.to(device=w.q.device, dtype=out_dtype).contiguous()
-        self.w8 = _decode(self.dw, w.group_size)
+        self._w8: Optional[torch.Tensor] = None
         self.lib = _lib.load()
+        g = w.group_size
+        self.few_rows_ok = (self.k % 64 == 0 and (g in (16, 32) or g % 64 == 0) and self.k % g == 0
+                            and self.dw.q.data_ptr() % 16 == 0 and self.dw.ldq % 16 == 0)
+
+    @property
+    def w8(self) -> torch.Tensor:
+        if self._w8 is None:
+            self._w8 = _decode(self.dw, self.w.group_size)
+        return self._w8
 
     def __call__(self, x2: torch.Tensor, out: torch.Tensor) -> None:
         (self._a8 if self.precision == "a8" else self._a16)(x2, out)
@@ -259,6 +273,16 @@ class _HipRunner:
     def gemm(self, xq: torch.Tensor, xs: torch.Tensor, out: torch.Tensor) -> None:
         """The int8 GEMM with the fused epilogue on quantised activations xq [m, K], scales xs [m, 1]."""
         m = xq.shape[0]
+        if m <= FEW_ROWS and self.few_rows_ok:
+            dw = self.dw
+            nbytes = self.lib.h3k_gemm_w4a8_workspace(m, self.n, self.k)
+            ws = torch.empty(max(1, nbytes // 4), dtype=torch.int32, device=xq.device) if nbytes else None
+            _lib.check(self.lib.h3k_gemm_w4a8(xq.data_ptr(), self.k, xs.data_ptr(), dw.q.data_ptr(), dw.ldq,
+                                              dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(), self.w.group_size,
+                                              dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
+                                              _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0),
+                                              _lib.ptr(ws), None, _lib.stream_of(xq.device)), "h3k_gemm_w4a8")
+            return
         _lib.check(self.lib.h3k_gemm_a8w8(xq.data_ptr(), self.k, xs.data_ptr(), self.w8.data_ptr(), self.k,
                                           self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
                                           _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0), None,

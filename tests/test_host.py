@@ -65,6 +65,16 @@ def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     assert lib.h3k_rms_modulate(None, 100, 4, 100, None, None, None, 100, None, 1e-5, None, 100, None) == _lib.EINVAL
     assert "multiple of 8" in lib.h3k_last_error().decode()
     assert lib.h3k_rms_modulate(None, 5120, 0, 5120, None, None, None, 5120, None, 1e-5, None, 5120, None) == 0
+    # fused few-row W4A8 GEMM: at most 128 rows, k a multiple of 64, group 16 / 32 / multiple of 64
+    w4 = lambda m, k, group: lib.h3k_gemm_w4a8(None, k, None, None, k // 2, None, _lib.FP8E4M3, max(1, k // group),  # noqa: E731
+                                               None, group, None, None, m, 64, k, 0, None, _lib.BF16, 64, None, None,
+                                               None)
+    assert w4(129, 512, 16) == _lib.EINVAL and "rows" in lib.h3k_last_error().decode()
+    assert w4(8, 544, 32) == _lib.EINVAL and "multiple of 64" in lib.h3k_last_error().decode()
+    assert w4(8, 512, 8) == _lib.EINVAL and "group_size" in lib.h3k_last_error().decode()
+    assert w4(0, 512, 16) == 0
+    assert lib.h3k_gemm_w4a8_workspace(64, 256, 5120) == 64 * 256 * 4  # split K: int32 accumulators
+    assert lib.h3k_gemm_w4a8_workspace(64, 256, 256) == 0
 
 
 def make_weight(n=40, k=512, group=16):
