@@ -115,6 +115,18 @@ int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * h3k_rotate_quant of an activation applied as the input is read, in one pass:
+ *   act 1 (swiglu): x rows are [gate | up] (2k wide); the quantised input is silu(gate) * up, each op rounded to
+ *                   the activation dtype -- replaces qlinear.py:376-379 (_swiglu) + :295-303 (quantize_activation)
+ *                   for fc2's input (input_act="swiglu", qlinear.py:494-501)
+ *   act 2 (gelu_tanh): the quantised input is gelu(x, tanh approximation) rounded to the activation dtype (the
+ *                   config-4 GELU block's fc2 input; no reference counterpart, the reference block is SwiGLU)
+ * bf16/f16 x, rotation 256, k a multiple of 256 up to 32768; 16-byte aligned rows.
+ */
+int h3k_rotate_quant_act(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int act, int rot, int mode,
+                         int8_t* q, int64_t ldq, float* xs, void* stream);
+
+/*
  * Per-head RMSNorm + split-half rotary embedding of q and k, in place, bf16.
  * Replaces h3turbo/h3/layout.py:329-355 (norm_rope_, impl "torch": the numerics of comfy_kitchen's fused
  * rms_rope_split_half_ called at :339, which the reference reproduces with rms_norm_fused_order, :309-326).

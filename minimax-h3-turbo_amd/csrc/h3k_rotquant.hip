@@ -48,6 +48,45 @@ __device__ __forceinline__ uint32_t round_bits_16(float f) {
   return F16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f);
 }
 
+// Activations applied to the input as it is loaded (ACT 1: [gate | up] rows, silu(gate) * up; ACT 2: tanh GELU),
+// each op rounded to the activation dtype like the torch ops they replace: F.silu(gate).mul_(up) (reference
+// h3turbo/h3/qlinear.py:376-379) and F.gelu(x, approximate="tanh"), both with fp32 math.
+constexpr int kActNone = 0, kActSwiglu = 1, kActGeluTanh = 2;
+
+template <bool F16>
+__device__ __forceinline__ float round16(float f) {
+  return F16 ? round_f16(f) : round_bf16(f);
+}
+
+template <bool F16>
+__device__ __forceinline__ uint32_t swiglu_word(uint32_t g2, uint32_t u2) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float g = to_f32_16<F16>((g2 >> (16 * h)) & 0xFFFFu), u = to_f32_16<F16>((u2 >> (16 * h)) & 0xFFFFu);
+    const float d = fp32_round_point(1.0f + expf(-g));
+    const float sl = round16<F16>(fp32_round_point(g / d));
+    r |= round_bits_16<F16>(fp32_round_point(sl * u)) << (16 * h);
+  }
+  return r;
+}
+
+template <bool F16>
+__device__ __forceinline__ uint32_t gelu_tanh_word(uint32_t x2) {
+  constexpr float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
+  constexpr float kKappa = 0.044715f;
+  uint32_t r = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float x = to_f32_16<F16>((x2 >> (16 * h)) & 0xFFFFu);
+    const float cube = fp32_round_point(fp32_round_point(x * x) * x);
+    const float inner = fp32_round_point(kBeta * fp32_round_point(x + fp32_round_point(kKappa * cube)));
+    const float y = fp32_round_point(fp32_round_point(0.5f * x) * fp32_round_point(1.0f + tanhf(inner)));
+    r |= round_bits_16<F16>(y) << (16 * h);
+  }
+  return r;
+}
+
 // LDS geometry of the fast path (per wave, per 16-lane group g)
 constexpr int kInStride = 16 * 16 + 16;  // uint16 per group: 16 rows of 16 + pad (skews groups by 8 banks)
 constexpr int kMidRow = 17;              // doubles per mid-transpose row (odd: conflict-free 64-bit access)
@@ -58,7 +97,7 @@ constexpr int kMidStride = 16 * kMidRow + 4;
 // Row layout: element e of row r is at x[r * ldx + (e >> hshift) * hstride + (e & (2^hshift - 1))]; hshift = 31
 // is a plain row, hshift = log2(head_dim) reads a head-major [heads, rows, head_dim] tensor as rows of
 // heads * head_dim (head_dim >= 16, so a lane's 16 consecutive elements stay inside one head).
-template <int NPASS, int WPR, bool F16, bool EAGER>
+template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone>
 __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __restrict__ x, int64_t rows, int k,
                                                           int64_t ldx, int hshift, int64_t hstride,
                                                           int8_t* __restrict__ q, int64_t ldq, float* __restrict__ xs) {
@@ -86,6 +125,21 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
                                                         (e & ((1 << hshift) - 1)));
       raw[p][0] = __builtin_nontemporal_load(src);
       raw[p][1] = __builtin_nontemporal_load(src + 1);
+      if (ACT == kActSwiglu) {  // plain rows of 2k: gate at e, up at k + e
+        const u32x4* up = reinterpret_cast<const u32x4*>(xr + k + e);
+        const u32x4 u0 = __builtin_nontemporal_load(up), u1 = __builtin_nontemporal_load(up + 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          raw[p][0][i] = swiglu_word<F16>(raw[p][0][i], u0[i]);
+          raw[p][1][i] = swiglu_word<F16>(raw[p][1][i], u1[i]);
+        }
+      } else if (ACT == kActGeluTanh) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          raw[p][0][i] = gelu_tanh_word<F16>(raw[p][0][i]);
+          raw[p][1][i] = gelu_tanh_word<F16>(raw[p][1][i]);
+        }
+      }
     } else {
       raw[p][0] = u32x4{0, 0, 0, 0};
       raw[p][1] = u32x4{0, 0, 0, 0};
@@ -257,11 +311,11 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
 }
 
 // ------------------------------------------------------------------------------------------------ host side
-template <int NPASS, int WPR, bool F16, bool EAGER>
+template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone>
 static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int hshift, int64_t hstride, int8_t* q,
                       int64_t ldq, float* xs, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>((rows + (4 / WPR) - 1) / (4 / WPR)));
-  hipLaunchKernelGGL((rotquant256_kernel<NPASS, WPR, F16, EAGER>), grid, dim3(256), 0, st,
+  hipLaunchKernelGGL((rotquant256_kernel<NPASS, WPR, F16, EAGER, ACT>), grid, dim3(256), 0, st,
                      static_cast<const uint16_t*>(x), rows, k, ldx, hshift, hstride, q, ldq, xs);
 }
 
@@ -283,13 +337,13 @@ static void rq_plan(int blocks, int64_t rows, int& npass, int& wpr) {
     }
 }
 
-template <bool F16, bool EAGER>
+template <bool F16, bool EAGER, int ACT = kActNone>
 static bool dispatch256(int npass, int wpr, const void* x, int64_t rows, int k, int64_t ldx, int hshift,
                         int64_t hstride, int8_t* q, int64_t ldq, float* xs, hipStream_t st) {
   switch (npass * 8 + wpr) {
 #define H3K_CASE(P, W)      \
   case P * 8 + W:           \
-    launch256<P, W, F16, EAGER>(x, rows, k, ldx, hshift, hstride, q, ldq, xs, st); \
+    launch256<P, W, F16, EAGER, ACT>(x, rows, k, ldx, hshift, hstride, q, ldq, xs, st); \
     return true;
     H3K_CASE(1, 1) H3K_CASE(2, 1) H3K_CASE(3, 1) H3K_CASE(4, 1) H3K_CASE(5, 1) H3K_CASE(6, 1) H3K_CASE(7, 1)
     H3K_CASE(8, 1) H3K_CASE(1, 4) H3K_CASE(2, 4) H3K_CASE(3, 4) H3K_CASE(4, 4) H3K_CASE(5, 4) H3K_CASE(6, 4)
@@ -402,6 +456,40 @@ extern "C" int h3k_rotate_quant_heads(const void* x, int x_dtype, int64_t rows, 
                : dispatch256<false, false>(np, wpr, x, rows, kk, ldx, hshift, head_stride, q, ldq, xs, st);
   if (!ok) return fail(H3K_EINVAL, "no fast rotation kernel for k=%lld", (long long)k);
   return check_launch("rotquant256(heads)");
+}
+
+extern "C" int h3k_rotate_quant_act(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int act,
+                                    int rot, int mode, int8_t* q, int64_t ldq, float* xs, void* stream) {
+  if (act != kActSwiglu && act != kActGeluTanh) return fail(H3K_EINVAL, "act must be 1 (swiglu) or 2 (gelu_tanh), got %d", act);
+  if (x_dtype != H3K_BF16 && x_dtype != H3K_F16)
+    return fail(H3K_EINVAL, "activation-fused rows take bf16 or f16 inputs (dtype code %d)", x_dtype);
+  if (rot != 256) return fail(H3K_EINVAL, "activation-fused rows take rotation 256, got %d", rot);
+  if (mode != H3K_MODE_CK && mode != H3K_MODE_EAGER) return fail(H3K_EINVAL, "mode must be ck (0) or eager (1)");
+  if (rows < 0 || k <= 0 || k % 256) return fail(H3K_EINVAL, "k=%lld must be a positive multiple of 256", (long long)k);
+  const int64_t width = act == kActSwiglu ? 2 * k : k;
+  if (ldx < width) return fail(H3K_EINVAL, "ldx=%lld < input width %lld", (long long)ldx, (long long)width);
+  if (ldq < k) return fail(H3K_EINVAL, "ldq=%lld < k=%lld", (long long)ldq, (long long)k);
+  int np = 0, wpr = 1;
+  if (k <= (int64_t)256 * 128) rq_plan(static_cast<int>(k / 256), rows, np, wpr);
+  if (np == 0) return fail(H3K_EINVAL, "k=%lld too long for the activation-fused kernel", (long long)k);
+  if (rows == 0) return H3K_OK;
+  if (!x || !q || !xs) return fail(H3K_EINVAL, "x/q/xs is NULL");
+  if (!aligned(x, 16) || (ldx * 2) % 16 || !aligned(q, 16) || ldq % 16)
+    return fail(H3K_EINVAL, "x / q and their row strides must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool eager = mode == H3K_MODE_EAGER, f16 = x_dtype == H3K_F16;
+  const int kk = static_cast<int>(k);
+  bool ok;
+#define H3K_ACT(F, E, A) dispatch256<F, E, A>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st)
+  if (act == kActSwiglu)
+    ok = f16 ? (eager ? H3K_ACT(true, true, kActSwiglu) : H3K_ACT(true, false, kActSwiglu))
+             : (eager ? H3K_ACT(false, true, kActSwiglu) : H3K_ACT(false, false, kActSwiglu));
+  else
+    ok = f16 ? (eager ? H3K_ACT(true, true, kActGeluTanh) : H3K_ACT(true, false, kActGeluTanh))
+             : (eager ? H3K_ACT(false, true, kActGeluTanh) : H3K_ACT(false, false, kActGeluTanh));
+#undef H3K_ACT
+  if (!ok) return fail(H3K_EINVAL, "no fast rotation kernel for k=%lld", (long long)k);
+  return check_launch("rotquant256(act)");
 }
 
 extern "C" int h3k_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot, void* y,

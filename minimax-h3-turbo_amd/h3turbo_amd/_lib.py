@@ -29,6 +29,7 @@ SIGNATURES = {
     "h3k_rotate": (_int, [_ptr, _int, _i64, _i64, _i64, _int, _ptr, _i64, _ptr]),
     "h3k_decode_w4": (_int, [_ptr, _i64, _ptr, _int, _i64, _ptr, _i64, _i64, _int, _ptr, _i64, _ptr]),
     "h3k_gemm_a8w8": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _int, _ptr, _int, _i64, _ptr, _ptr]),
+    "h3k_rotate_quant_act": (_int, [_ptr, _int, _i64, _i64, _i64, _int, _int, _int, _ptr, _i64, _ptr, _ptr]),
     "h3k_gemm_w4a8_workspace": (_i64, [_i64, _i64, _i64]),
     "h3k_gemm_w4a8": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _int, _i64, _ptr, _int, _ptr, _ptr, _i64, _i64, _i64,
                              _int, _ptr, _int, _i64, _ptr, _ptr, _ptr]),

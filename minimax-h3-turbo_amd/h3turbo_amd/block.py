@@ -266,8 +266,7 @@ class DiTBlock:
     def linear(self, x: torch.Tensor, w: Weight, input_act: Optional[str] = None) -> torch.Tensor:
         """One of the block's four large linears (h3turbo/h3/model.py:179-184)."""
         if isinstance(w, torch.Tensor):  # dense weight: plain F.linear in x.dtype
-            if input_act == "swiglu":
-                x = qlinear._swiglu(x)
+            x = qlinear.apply_input_act(x, input_act)
             return F.linear(x, w if w.dtype == x.dtype else w.to(x.dtype))
         return qlinear.linear(x, w, backend=self.backend, precision=self.precision, input_act=input_act,
                               quant_mode=self.quant_mode)
@@ -278,7 +277,7 @@ class DiTBlock:
             z = self.linear(hc, w.fc1)
             if self.cfg.act == "swiglu":
                 return self.linear(z, w.fc2, "swiglu")
-            return self.linear(F.gelu(z, approximate="tanh"), w.fc2)
+            return self.linear(z, w.fc2, "gelu_tanh")  # W4A8 a8: the GELU runs inside rotate+quantise
 
         s = h.shape[0]
         step = self.mlp_chunk or s

@@ -230,6 +230,20 @@ def resolve_backend(x: torch.Tensor, w: Weight, backend: str = "auto", precision
     return "hip"
 
 
+INPUT_ACTS = (None, "none", "swiglu", "gelu_tanh")
+ACT_CODE = {"swiglu": 1, "gelu_tanh": 2}
+
+
+def apply_input_act(x: torch.Tensor, act: Optional[str]) -> torch.Tensor:
+    """The input activation as torch ops in x.dtype: "swiglu" (qlinear.py:376-379) or "gelu_tanh"
+    (F.gelu(x, approximate="tanh"), the config-4 block's MLP; an extension of the reference's input_act)."""
+    if act == "swiglu":
+        return _swiglu(x)
+    if act == "gelu_tanh":
+        return F.gelu(x, approximate="tanh")
+    return x
+
+
 def _swiglu(x: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up on [gate | up] halves, in x.dtype (qlinear.py:376-379)."""
     gate, up = x.chunk(2, dim=-1)
@@ -263,12 +277,26 @@ class _HipRunner:
             self._w8 = _decode(self.dw, self.w.group_size)
         return self._w8
 
-    def __call__(self, x2: torch.Tensor, out: torch.Tensor) -> None:
-        (self._a8 if self.precision == "a8" else self._a16)(x2, out)
+    def __call__(self, x2: torch.Tensor, out: torch.Tensor, act: Optional[str] = None) -> None:
+        if self.precision == "a8":
+            self._a8(x2, out, act)
+        else:
+            self._a16(apply_input_act(x2, act), out)
 
-    def _a8(self, x2: torch.Tensor, out: torch.Tensor) -> None:
-        xq, xs = _quantize_rows(x2, self.w.convrot, self.mode)
+    def _a8(self, x2: torch.Tensor, out: torch.Tensor, act: Optional[str] = None) -> None:
+        if act in ACT_CODE and self._act_fused_ok(x2, act):
+            xq, xs = _quantize_rows_act(x2, ACT_CODE[act], self.k, self.mode)
+        else:
+            xq, xs = _quantize_rows(apply_input_act(x2, act), self.w.convrot, self.mode)
         self.gemm(xq, xs, out)
+
+    def _act_fused_ok(self, x2: torch.Tensor, act: str) -> bool:
+        """The activation runs inside rotate+quantise (h3k_rotate_quant_act): 16-bit rows, rotation 256."""
+        k = self.k
+        width = 2 * k if act == "swiglu" else k
+        return (x2.dtype in (torch.bfloat16, torch.float16) and self.w.convrot == 256 and k % 256 == 0
+                and k <= 256 * 128 and x2.shape[-1] == width and x2.stride(-1) == 1 and x2.data_ptr() % 16 == 0
+                and (x2.shape[0] <= 1 or (x2.stride(0) * 2) % 16 == 0))
 
     def gemm(self, xq: torch.Tensor, xs: torch.Tensor, out: torch.Tensor) -> None:
         """The int8 GEMM with the fused epilogue on quantised activations xq [m, K], scales xs [m, 1]."""
@@ -299,8 +327,23 @@ class _HipRunner:
         out.copy_(y)
 
 
+def _quantize_rows_act(x2: torch.Tensor, act_code: int, k: int, mode: str) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Rotate + quantise act(x2) in one pass (h3k_rotate_quant_act): (int8 [M, k], fp32 [M, 1])."""
+    m = x2.shape[0]
+    q = torch.empty(m, k, dtype=torch.int8, device=x2.device)
+    xs = torch.empty(m, 1, dtype=torch.float32, device=x2.device)
+    if m == 0:
+        return q, xs
+    lib = _lib.load()
+    _lib.check(lib.h3k_rotate_quant_act(x2.data_ptr(), _lib.act_code(x2.dtype), m, k, _ld(x2), act_code, CONVROT,
+                                        _lib.MODE[mode], q.data_ptr(), k, xs.data_ptr(), _lib.stream_of(x2.device)),
+               "h3k_rotate_quant_act")
+    return q, xs
+
+
 @torch.no_grad()
-def _linear_w4a8(x2, w, bias, out_dtype, backend, precision, swiglu, chunk_tokens, quant_mode):
+def _linear_w4a8(x2, w, bias, out_dtype, backend, precision, act, chunk_tokens, quant_mode):
+    swiglu = act == "swiglu"
     n, k = _check_weight(w)
     kx = x2.shape[-1] // (2 if swiglu else 1)
     if kx != k:
@@ -320,10 +363,7 @@ def _linear_w4a8(x2, w, bias, out_dtype, backend, precision, swiglu, chunk_token
     runner = _HipRunner(w, bias, out_dtype, precision, quant_mode)
     step = min(chunk_tokens or m, m)
     for a in range(0, m, step):
-        xc = x2[a: a + step]
-        if swiglu:
-            xc = _swiglu(xc)
-        runner(xc, out[a: a + step])
+        runner(x2[a: a + step], out[a: a + step], act)
     return out
 
 
@@ -384,12 +424,14 @@ def linear(
     w: dense [N, K] tensor (plain F.linear in x.dtype) or W4A8Weight (HIP kernels).
     precision "a8" quantises activations to int8 per token (the native W4A8 path); "a16" keeps them (rotated x
     times the exact int8 levels, fp32 accumulation).  input_act="swiglu": x is [gate | up], silu(gate) * up in
-    x.dtype first.  chunk_tokens bounds peak memory; a8 is token-wise, so chunking is bit-exact.
+    x.dtype first; "gelu_tanh" (an extension for the config-4 block): tanh-approximate GELU in x.dtype.  On the
+    W4A8 a8 path the activation runs inside the rotate+quantise kernel.  chunk_tokens bounds peak memory; a8 is
+    token-wise, so chunking is bit-exact.
     """
     if not x.is_floating_point():
         raise ValueError(f"x must be floating point, got {x.dtype}")
-    if input_act not in (None, "none", "swiglu"):
-        raise ValueError(f"input_act must be None or 'swiglu', got {input_act!r}")
+    if input_act not in INPUT_ACTS:
+        raise ValueError(f"input_act must be None, 'swiglu' or 'gelu_tanh', got {input_act!r}")
     if chunk_tokens is not None and chunk_tokens < 1:
         raise ValueError("chunk_tokens must be >= 1")
     _check_mode(quant_mode)
@@ -401,7 +443,8 @@ def linear(
     lead = x.shape[:-1]
     x2 = x.reshape(math.prod(lead), x.shape[-1])
     if kind != "dense":
-        y = _linear_w4a8(x2, w, bias, out_dtype, backend, precision, swiglu, chunk_tokens, quant_mode)
+        y = _linear_w4a8(x2, w, bias, out_dtype, backend, precision, None if input_act == "none" else input_act,
+                         chunk_tokens, quant_mode)
         return y.reshape(*lead, y.shape[-1])
     if x2.shape[-1] // (2 if swiglu else 1) != w.shape[-1]:
         raise ValueError(f"input features {x2.shape[-1]} do not match the dense weight {tuple(w.shape)}")
@@ -411,9 +454,7 @@ def linear(
     bd = None if bias is None else bias.to(dtype=wd.dtype)
     outs = []
     for a in range(0, max(x2.shape[0], 1), step):
-        xc = x2[a: a + step]
-        if swiglu:
-            xc = _swiglu(xc)
+        xc = apply_input_act(x2[a: a + step], input_act)
         outs.append(F.linear(xc.to(wd.dtype), wd, bd).to(out_dtype))
     y = outs[0] if len(outs) == 1 else torch.cat(outs, 0)
     return y.reshape(*lead, y.shape[-1])

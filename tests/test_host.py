@@ -75,6 +75,15 @@ def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     assert w4(0, 512, 16) == 0
     assert lib.h3k_gemm_w4a8_workspace(64, 256, 5120) == 64 * 256 * 4  # split K: int32 accumulators
     assert lib.h3k_gemm_w4a8_workspace(64, 256, 256) == 0
+    # activation-fused rotate+quant: 16-bit input, act 1 or 2, rotation 256, the full input width per row
+    act = lambda dt, k, ldx, a, rot=256: lib.h3k_rotate_quant_act(None, dt, 4, k, ldx, a, rot, 0, None, k, None,  # noqa: E731
+                                                                  None)
+    assert act(_lib.F32, 256, 256, 2) == _lib.EINVAL and "bf16 or f16" in lib.h3k_last_error().decode()
+    assert act(_lib.BF16, 256, 256, 3) == _lib.EINVAL and "act" in lib.h3k_last_error().decode()
+    assert act(_lib.BF16, 256, 256, 2, rot=64) == _lib.EINVAL and "rotation 256" in lib.h3k_last_error().decode()
+    assert act(_lib.BF16, 256, 256, 1) == _lib.EINVAL and "ldx" in lib.h3k_last_error().decode()
+    assert act(_lib.BF16, 256 * 129, 256 * 129, 2) == _lib.EINVAL and "too long" in lib.h3k_last_error().decode()
+    assert lib.h3k_rotate_quant_act(None, _lib.F16, 0, 512, 1024, 1, 256, 1, None, 512, None, None) == 0
 
 
 def make_weight(n=40, k=512, group=16):
