@@ -352,6 +352,278 @@ __global__ __launch_bounds__(256) void gemm_w4_col_kernel(const int8_t* __restri
   }
 }
 
+// ------------------------------------------------------------------------------------------------ 16-row tiles
+// Up to 16 rows with K a multiple of 128 and enough columns to fill the chip (gemm_w4_c16_kernel).
+//
+// v_mfma_i32_16x16x64_i8 takes 16 rows of A per fragment, so 16 rows need no padding and one A fragment feeds the
+// two 16-column groups of a wavefront's 32 columns.  A super-step is 128 k: lane group g = lane / 16 takes the 32
+// consecutive k [128t + 32g, 128t + 32g + 32) of its column (one 16-byte load of packed weight) and splits them over
+// the two MFMA sub-steps (k + [0, 16), k + [16, 32)); its A fragments take the same k of its row (any permutation of
+// k applied to both operands leaves the sums unchanged).  So the four lanes of a column share a scale wherever the
+// group spans 128 k (64: pairs of lanes): each builds one word (two) of the 16-byte table and they exchange words
+// through ds_bpermute.  The table level is clamp(rint(c * s)) with the rounding done by adding 1.5 * 2^23 (the sum
+// is an integer in [2^23, 2^24), its low byte the two's-complement level).
+//
+// A workgroup of 8 wavefronts owns 32 columns; the wavefronts split K in eight and meet in LDS (fixed order).
+// Loads go through buffer descriptors: one 32-bit lane offset per operand, the step in the scalar offset, so the
+// K loop spends no VALU on addresses.  Chunks of kC16Chunk super-steps are double-buffered in registers.
+constexpr int kC16Waves = 8;
+constexpr int kSS = 128;        // k per super-step
+constexpr int kC16Chunk = 2;    // super-steps per register chunk
+constexpr int kC16MinTiles = 128;  // fewer 32-column tiles leave the chip idle: the split-K column kernel serves
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
+                                                                         static_cast<int>(soff), 0));
+}
+
+template <int SD>
+__device__ __forceinline__ uint32_t bload_scale_bits(rsrc_t r, uint32_t voff, uint32_t soff) {
+  if (SD == H3K_FP8E4M3) return __builtin_amdgcn_raw_buffer_load_b8(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+  if (SD == H3K_F16 || SD == H3K_BF16)
+    return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+
+template <int SD>
+__device__ __forceinline__ float scale_value(uint32_t bits) {
+  if (SD == H3K_FP8E4M3) return fp8e4m3fn_to_f32(bits);
+  if (SD == H3K_F16) return f16_to_f32(bits);
+  if (SD == H3K_BF16) return bf16_to_f32(bits);
+  return __uint_as_float(bits);
+}
+
+template <int SD>
+constexpr int scale_bytes() {
+  return SD == H3K_FP8E4M3 ? 1 : (SD == H3K_F32 ? 4 : 2);
+}
+
+// level(c, s) + 1.5 * 2^23 for a finite product: the low byte is the level.
+__device__ __forceinline__ uint32_t level_addend(float cbv, float s) {
+  const float p = __builtin_amdgcn_fmed3f(fp32_round_point(cbv * s), -127.0f, 127.0f);
+  return __float_as_uint(fp32_round_point(p + 12582912.0f));
+}
+
+// Table word of codebook entries c[0..3] at scale s (byte i = level(c[i], s)); the NaN-aware form unless every
+// product is finite.
+__device__ __forceinline__ uint32_t lut_word(const float* c, float s, bool fast) {
+  if (fast) {
+    const uint32_t b0 = level_addend(c[0], s), b1 = level_addend(c[1], s), b2 = level_addend(c[2], s),
+                   b3 = level_addend(c[3], s);
+    return __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);
+  }
+  return level(c[0], s) | (level(c[1], s) << 8) | (level(c[2], s) << 16) | (level(c[3], s) << 24);
+}
+
+template <int MR, int GK>
+struct C16Chunk {
+  u32x4 pq[kC16Chunk][2];              // [super-step][column group]: 32 packed k of the lane's column
+  u32x4 pa[kC16Chunk][MR][2];          // [super-step][row group][sub-step]: 16 k of the lane's row
+  uint32_t s[kC16Chunk][2][GK == 16 ? 2 : 1];  // raw scale bits [super-step][column group][16-k half]
+};
+
+struct C16Lanes {
+  rsrc_t rq, ra, rs;
+  uint32_t qv[2];   // byte offsets of the lane's packed k in its two columns
+  uint32_t av[2];   // byte offsets of the lane's k in its row of each row group
+  uint32_t sv[2];   // byte offsets of the lane's first scale in its two columns
+};
+
+// Super-steps first .. first + kC16Chunk - 1 of the wavefront's range (ss0 + ..); slots past nss reload the last
+// valid super-step and are not computed.
+template <int MR, int SD, int GK>
+__device__ __forceinline__ void c16_load(C16Chunk<MR, GK>& c, int first, int nss, int ss0, const C16Lanes& L,
+                                         int group) {
+  constexpr uint32_t sb = scale_bytes<SD>();
+#pragma unroll
+  for (int j = 0; j < kC16Chunk; ++j) {
+    const int ss = ss0 + min(first + j, nss - 1);
+#pragma unroll
+    for (int cg = 0; cg < 2; ++cg) c.pq[j][cg] = bload16(L.rq, L.qv[cg], static_cast<uint32_t>(ss) * (kSS / 2));
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) c.pa[j][r][s] = bload16(L.ra, L.av[r] + s * 16, static_cast<uint32_t>(ss) * kSS);
+    uint32_t sidx;  // uniform part of the scale index
+    if (GK == 128) sidx = static_cast<uint32_t>(ss * kSS / group);
+    else sidx = static_cast<uint32_t>(ss) * (kSS / GK);
+#pragma unroll
+    for (int cg = 0; cg < 2; ++cg) {
+      c.s[j][cg][0] = bload_scale_bits<SD>(L.rs, L.sv[cg], sidx * sb);
+      if (GK == 16) c.s[j][cg][GK == 16 ? 1 : 0] = bload_scale_bits<SD>(L.rs, L.sv[cg] + sb, sidx * sb);
+    }
+  }
+}
+
+template <int MR, int SD, int GK, int NCB>
+__device__ __forceinline__ void c16_compute(const C16Chunk<MR, GK>& c, int first, int nss, int ss0,
+                                            const float (&cbw)[NCB], bool cbw_finite, const uint32_t (&bp)[2],
+                                            uint32_t (&lut)[2][4], uint32_t (&lut2)[2][4], v4i (&acc)[MR][2],
+                                            int group) {
+#pragma unroll
+  for (int j = 0; j < kC16Chunk; ++j) {
+    const int i = first + j;
+    if (i >= nss) break;  // uniform
+    const int ss = ss0 + i;
+    const bool rebuild = GK != 128 || i == 0 || (ss * kSS) % group == 0;  // uniform
+    if (rebuild) {
+#pragma unroll
+      for (int cg = 0; cg < 2; ++cg) {
+        const float s = scale_value<SD>(c.s[j][cg][0]);
+        const bool fast = cbw_finite && __builtin_isfinite(s);
+        if (GK == 128) {  // this lane built word g; word w comes from lane group w of the column
+          const uint32_t x = lut_word(&cbw[0], s, fast);
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            lut[cg][w] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp[0] + 64 * w),
+                                                                            static_cast<int>(x)));
+        } else if (GK == 64) {  // this lane built words 2h, 2h + 1 (h = g & 1); the pair is lane groups g & 2, +1
+          const uint32_t x0 = lut_word(&cbw[0], s, fast), x1 = lut_word(&cbw[4], s, fast);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            lut[cg][2 * h] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp[h]), static_cast<int>(x0)));
+            lut[cg][2 * h + 1] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp[h]), static_cast<int>(x1)));
+          }
+        } else {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) lut[cg][w] = lut_word(&cbw[4 * w], s, fast);
+          if (GK == 16) {
+            const float s2 = scale_value<SD>(c.s[j][cg][GK == 16 ? 1 : 0]);
+            const bool fast2 = cbw_finite && __builtin_isfinite(s2);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) lut2[cg][w] = lut_word(&cbw[4 * w], s2, fast2);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int cg = 0; cg < 2; ++cg) {
+      v4i bf[2];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        uint32_t lo4, hi4;
+        if (GK == 16 && w >= 2) lut_decode_word(lut2[cg], c.pq[j][cg][w], lo4, hi4);
+        else lut_decode_word(lut[cg], c.pq[j][cg][w], lo4, hi4);
+        bf[w >> 1][(w & 1) * 2] = static_cast<int>(lo4);
+        bf[w >> 1][(w & 1) * 2 + 1] = static_cast<int>(hi4);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          const u32x4 a = c.pa[j][r][s];
+          const v4i af = {static_cast<int>(a[0]), static_cast<int>(a[1]), static_cast<int>(a[2]), static_cast<int>(a[3])};
+          acc[r][cg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[s], acc[r][cg], 0, 0, 0);
+        }
+    }
+  }
+}
+
+template <int MR, int SD, int GK>
+__global__ __launch_bounds__(512) void gemm_w4_c16_kernel(const int8_t* __restrict__ A, int64_t lda,
+                                                          const float* __restrict__ xs, const uint8_t* __restrict__ q,
+                                                          int64_t ldq, const void* __restrict__ s_rel, int64_t lds,
+                                                          const float* __restrict__ cb, int group,
+                                                          const float* __restrict__ sch, const void* __restrict__ bias,
+                                                          int M, int N, int K, int wss, void* __restrict__ out,
+                                                          int64_t ldo, int odt, bool eager,
+                                                          int32_t* __restrict__ acc_out) {
+  constexpr int R = MR * 8;  // accumulator registers per lane
+  __shared__ int32_t red[kC16Waves][R][64];
+  constexpr uint32_t sb = scale_bytes<SD>();
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c16 = lane & 15;
+  const int KS = K / kSS;
+  const int ss0 = wave * wss;
+  const int nss = max(0, min(wss, KS - ss0));
+
+  C16Lanes L;
+  L.rq = make_rsrc(q, static_cast<uint32_t>(static_cast<int64_t>(N - 1) * ldq + K / 2));
+  L.ra = make_rsrc(A, static_cast<uint32_t>(static_cast<int64_t>(M - 1) * lda + K));
+  L.rs = make_rsrc(s_rel, static_cast<uint32_t>((static_cast<int64_t>(N - 1) * lds + K / group) * sb));
+#pragma unroll
+  for (int cg = 0; cg < 2; ++cg) {
+    const int col = min(blockIdx.x * 32 + cg * 16 + c16, N - 1);
+    L.qv[cg] = static_cast<uint32_t>(static_cast<int64_t>(col) * ldq + g * 16);
+    uint32_t sl = 0;  // the lane's part of the scale index
+    if (GK == 64) sl = g >> 1;
+    else if (GK == 32) sl = g;
+    else if (GK == 16) sl = 2 * g;
+    L.sv[cg] = static_cast<uint32_t>((static_cast<int64_t>(col) * lds + sl) * sb);
+  }
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    const int row = min(r * 16 + c16, M - 1);
+    L.av[r] = static_cast<uint32_t>(static_cast<int64_t>(row) * lda + g * 32);
+  }
+  if (MR == 1) L.av[1] = L.av[0];  // unused
+
+  constexpr int NCB = GK == 128 ? 4 : (GK == 64 ? 8 : 16);
+  float cbw[NCB];
+  const int cb0 = GK == 128 ? 4 * g : (GK == 64 ? 8 * (g & 1) : 0);
+#pragma unroll
+  for (int i = 0; i < NCB; ++i) cbw[i] = cb[cb0 + i];
+  bool cbw_finite = true;
+#pragma unroll
+  for (int i = 0; i < NCB; ++i) cbw_finite = cbw_finite && __builtin_isfinite(cbw[i]);
+  uint32_t bp[2];  // ds_bpermute byte addresses of the column's table builders
+  if (GK == 128) {
+    bp[0] = static_cast<uint32_t>(c16 * 4);
+    bp[1] = 0;
+  } else {
+    bp[0] = static_cast<uint32_t>((c16 + 16 * (g & 2)) * 4);
+    bp[1] = bp[0] + 64;
+  }
+
+  v4i acc[MR][2];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) acc[r][0] = acc[r][1] = v4i{0, 0, 0, 0};
+  uint32_t lut[2][4] = {}, lut2[2][4] = {};
+
+  C16Chunk<MR, GK> c0, c1;
+  if (nss > 0) c16_load<MR, SD, GK>(c0, 0, nss, ss0, L, group);
+  for (int first = 0; first < nss; first += 2 * kC16Chunk) {
+    if (first + kC16Chunk < nss) c16_load<MR, SD, GK>(c1, first + kC16Chunk, nss, ss0, L, group);
+    c16_compute<MR, SD, GK>(c0, first, nss, ss0, cbw, cbw_finite, bp, lut, lut2, acc, group);
+    if (first + 2 * kC16Chunk < nss) c16_load<MR, SD, GK>(c0, first + 2 * kC16Chunk, nss, ss0, L, group);
+    c16_compute<MR, SD, GK>(c1, first + kC16Chunk, nss, ss0, cbw, cbw_finite, bp, lut, lut2, acc, group);
+  }
+
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][(r * 2 + cg) * 4 + i][lane] = acc[r][cg][i];
+  __syncthreads();
+  // wavefront w finishes registers [w * MR, (w + 1) * MR) of every lane; C of 16x16: lane -> column lane % 16,
+  // register i -> row 4 * (lane / 16) + i
+#pragma unroll
+  for (int u = 0; u < R / kC16Waves; ++u) {
+    const int rr = wave * (R / kC16Waves) + u;
+    const int r = rr >> 3, cg = (rr >> 2) & 1, i = rr & 3;
+    const int m = r * 16 + g * 4 + i;
+    const int col = blockIdx.x * 32 + cg * 16 + c16;
+    if (m >= M || col >= N) continue;
+    int a = 0;
+#pragma unroll
+    for (int w = 0; w < kC16Waves; ++w) a += red[w][rr][lane];
+    const int64_t e = static_cast<int64_t>(m) * N + col;
+    if (acc_out) acc_out[e] = a;
+    store_out(odt, eager, a, xs[m], sch[col], bias ? load_bias(odt, bias, col) : 0.0f, bias != nullptr, out,
+              static_cast<int64_t>(m) * ldo + col);
+  }
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(u32x4* __restrict__ p, int64_t n16, int32_t* __restrict__ tail,
                                                    int64_t ntail) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -440,6 +712,41 @@ void launch(const Plan& p, int mode, int odt, const int8_t* a, int64_t lda, cons
                      bias, m, n, out, ldo, odt, eager, acc_out);
 }
 
+// gemm_w4_c16_kernel covers: up to 16 rows, K a multiple of 128, group 16 / 32 / 64 / a multiple of 128, at least
+// kC16MinTiles column tiles, and operands whose byte ranges fit a 31-bit buffer offset.  (Two row groups need 158
+// VGPRs, one workgroup per CU: 17-32 rows run faster on the 32-row column kernel.)
+inline bool c16_ok(int64_t m, int64_t n, int64_t k, int group, int64_t lda, int64_t ldq, int64_t lds, int sbytes) {
+  const int64_t lim = (int64_t{1} << 31) - 1;
+  return m >= 1 && m <= 16 && k % kSS == 0 && (group == 16 || group == 32 || group == 64 || group % kSS == 0) &&
+         (n + 31) / 32 >= kC16MinTiles && (m - 1) * lda + k <= lim && (n - 1) * ldq + k / 2 <= lim &&
+         ((n - 1) * lds + k / group) * sbytes <= lim;
+}
+
+template <int MR, int SD>
+void launch_c16_g(int mode, int odt, const int8_t* a, int64_t lda, const float* xs, const uint8_t* q, int64_t ldq,
+                  const void* s_rel, int64_t lds, const float* cb, int group, const float* sch, const void* bias, int m,
+                  int n, int k, void* out, int64_t ldo, int32_t* acc_out, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((n + 31) / 32));
+  const int ks = k / kSS;
+  const int wss = (ks + kC16Waves - 1) / kC16Waves;
+  const bool eager = mode == H3K_MODE_EAGER;
+#define H3K_C16(GK)                                                                                              \
+  hipLaunchKernelGGL((gemm_w4_c16_kernel<MR, SD, GK>), grid, dim3(64 * kC16Waves), 0, st, a, lda, xs, q, ldq, s_rel, \
+                     lds, cb, group, sch, bias, m, n, k, wss, out, ldo, odt, eager, acc_out)
+  if (group == 16) H3K_C16(16);
+  else if (group == 32) H3K_C16(32);
+  else if (group == 64) H3K_C16(64);
+  else H3K_C16(128);
+#undef H3K_C16
+}
+
+template <int SD>
+void launch_c16(int mode, int odt, const int8_t* a, int64_t lda, const float* xs, const uint8_t* q, int64_t ldq,
+                const void* s_rel, int64_t lds, const float* cb, int group, const float* sch, const void* bias, int m,
+                int n, int k, void* out, int64_t ldo, int32_t* acc_out, hipStream_t st) {
+  launch_c16_g<1, SD>(mode, odt, a, lda, xs, q, ldq, s_rel, lds, cb, group, sch, bias, m, n, k, out, ldo, acc_out, st);
+}
+
 template <int MB, int SD>
 void launch_g(const Plan& p, int mode, int odt, const int8_t* a, int64_t lda, const float* xs, const uint8_t* q,
               int64_t ldq, const void* s_rel, int64_t lds, const float* cb, int group, const float* sch,
@@ -490,13 +797,26 @@ extern "C" int h3k_gemm_w4a8(const int8_t* a, int64_t lda, const float* xs, cons
   if (!a || !xs || !q || !s_rel || !codebook || !s_ch || !out) return fail(H3K_EINVAL, "NULL pointer");
   if (!aligned(a, 16) || lda % 16 || !aligned(q, 16) || ldq % 16)
     return fail(H3K_EINVAL, "a and q must be 16-byte aligned with 16-byte multiple row strides");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
+  const uint8_t* qb = static_cast<const uint8_t*>(q);
+  const int sbytes = s_dtype == H3K_FP8E4M3 ? 1 : (s_dtype == H3K_F32 ? 4 : 2);
+  if (w4::c16_ok(m, n, k, group, lda, ldq, lds, sbytes)) {  // no workspace: K splits inside the workgroup
+#define H3K_C(SD) w4::launch_c16<SD>(mode, out_dtype, a, lda, xs, qb, ldq, s_rel, lds, codebook, group, s_ch, bias, \
+                                     mm, nn, kk, out, ldo, acc_out, st)
+    switch (s_dtype) {
+      case H3K_FP8E4M3: H3K_C(H3K_FP8E4M3); break;
+      case H3K_F16: H3K_C(H3K_F16); break;
+      case H3K_BF16: H3K_C(H3K_BF16); break;
+      default: H3K_C(H3K_F32); break;
+    }
+#undef H3K_C
+    return check_launch("gemm_w4a8(c16)");
+  }
   const w4::Plan p = w4::plan(m, n, k);
   if (p.splits > 1 && (!workspace || !aligned(workspace, 16)))
     return fail(H3K_EINVAL, "this shape splits K: pass a 16-byte aligned int32 workspace of "
                 "h3k_gemm_w4a8_workspace(m, n, k) bytes");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
-  const uint8_t* qb = static_cast<const uint8_t*>(q);
 #define H3K_M(SD) w4::launch_m<SD>(p, mode, out_dtype, a, lda, xs, qb, ldq, s_rel, lds, codebook, group, s_ch, bias, \
                                    mm, nn, kk, out, ldo, workspace, acc_out, st)
   switch (s_dtype) {

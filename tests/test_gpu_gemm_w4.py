@@ -1,7 +1,8 @@
 """The fused few-row W4A8 GEMM (h3k_gemm_w4a8: int4 decoded in registers, no int8 grid) through the C ABI, against
 the CPU oracle (decode_int8_grid, int8_mm, epilogue): every row count up to 128, ragged N, one K split and many, all
 group kinds (16, 32, multiples of 64), every scale dtype, NaN / clamp scales, both epilogue orders, every output
-dtype, bias, the accumulator dump, padded output rows.  Bit-exact."""
+dtype, bias, the accumulator dump, padded output rows; both kernels of up to 32 rows (32-row MFMA tiles for narrow N
+or K not a multiple of 128, 16-row tiles for up to 16 rows otherwise).  Bit-exact."""
 import numpy as np
 import pytest
 import torch
@@ -108,6 +109,41 @@ def test_split_and_unsplit_k():
     assert run(64, 256, 5120, group=128, acc=True, seed=5) > 0
     assert run(64, 256, 256, group=128, acc=True, seed=6) == 0
     assert run(128, 640, 5120, group=128, seed=7) > 0  # BASELINE K, 5 column tiles x 10 splits
+
+
+# 16-row MFMA tiles (gemm_w4_c16_kernel): up to 16 rows, K a multiple of 128, at least 128 tiles of 32 columns; the
+# same shapes with 17-32 rows run on the 32-row column kernel.
+C16_N = 4100  # 129 column tiles, the last one ragged
+
+
+@pytest.mark.parametrize("m", [1, 7, 16, 17, 32])
+def test_c16_every_row_group(m):
+    run(m, C16_N, 1152, group=128, seed=100 + m)  # 9 super-steps over 8 wavefronts: uneven K split
+
+
+@pytest.mark.parametrize("group,kind", [(16, "fp8"), (32, "bf16"), (64, "f32"), (128, "f16"), (256, "fp8"),
+                                        (512, "f16"), (384, "bf16")])
+def test_c16_groups_and_scale_kinds(group, kind):
+    k = 1536 if group == 384 else 1024
+    run(13, C16_N, k, group=group, kind=kind, seed=group + 1)
+    run(29, C16_N, k, group=group, kind=kind, seed=group + 2)
+
+
+@pytest.mark.parametrize("k", [128, 640, 5120])
+def test_c16_short_and_long_k(k):
+    run(16, C16_N, k, group=128, seed=k)  # one super-step (wave 0 alone), fewer than 8, the BASELINE K
+
+
+@pytest.mark.parametrize("mode", ["ck", "eager"])
+@pytest.mark.parametrize("odt", [_lib.BF16, _lib.F16, _lib.F32])
+def test_c16_epilogue_variants(mode, odt):
+    run(24, C16_N, 512, group=64, kind="fp8", mode=mode, odt=odt, with_bias=True, acc=True, ldo_pad=8, seed=33)
+
+
+@pytest.mark.parametrize("group", [16, 64, 128])
+def test_c16_non_finite_codebook_and_scales(group):
+    run(9, C16_N, 1024, group=group, kind="f32", seed=41, special=True)
+    run(30, C16_N, 1024, group=group, kind="f32", seed=42, special=True)
 
 
 def test_rejects_what_it_does_not_cover():
