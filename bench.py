@@ -459,7 +459,7 @@ def few_rows_measurement(dev, steps: int):
     128, fp16 scales) and the checkpoint format (group 16, fp8 scales), M in {16, 64, 128}.  The fused few-row GEMM
     (h3k_gemm_w4a8: int4 decoded in registers; zero-fill, GEMM and epilogue launches when it splits K) against the
     decode + int8 GEMM pair it replaces.  HBM figure = algorithmic bytes (packed weight + scales + int8 activations
-    + xs + s_ch + bf16 out) / time of the fused call, HIP events on the launch stream."""
+    + xs + s_ch + bf16 out) / time of the fused call: back-to-back calls between HIP events on the launch stream."""
     import torch
 
     from h3turbo_amd import _lib
@@ -473,17 +473,18 @@ def few_rows_measurement(dev, steps: int):
     rows = []
 
     def timed(fn):
+        # back-to-back calls between one pair of events: a single call of ~10-20 us bracketed by events would also
+        # time the dispatch gap in front of it
         for _ in range(3):
             _lib.check(fn(), "few rows")
-        evs = []
-        for _ in range(steps):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
+        reps = max(20, 4 * steps)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
             _lib.check(fn(), "few rows")
-            e1.record(stream)
-            evs.append((e0, e1))
+        e1.record(stream)
         torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in evs) / steps
+        return e0.elapsed_time(e1) / reps
 
     for fmt in ("g128_f16", "g16_fp8"):
         if fmt == "g128_f16":

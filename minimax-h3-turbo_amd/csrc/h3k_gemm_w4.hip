@@ -355,24 +355,27 @@ __global__ __launch_bounds__(256) void gemm_w4_col_kernel(const int8_t* __restri
 // ------------------------------------------------------------------------------------------------ 16-row tiles
 // Up to 16 rows with K a multiple of 128 and enough columns to fill the chip (gemm_w4_c16_kernel).
 //
-// v_mfma_i32_16x16x64_i8 takes 16 rows of A per fragment, so 16 rows need no padding and one A fragment feeds the
-// two 16-column groups of a wavefront's 32 columns.  A super-step is 128 k: lane group g = lane / 16 takes the 32
-// consecutive k [128t + 32g, 128t + 32g + 32) of its column (one 16-byte load of packed weight) and splits them over
-// the two MFMA sub-steps (k + [0, 16), k + [16, 32)); its A fragments take the same k of its row (any permutation of
-// k applied to both operands leaves the sums unchanged).  So the four lanes of a column share a scale wherever the
-// group spans 128 k (64: pairs of lanes): each builds one word (two) of the 16-byte table and they exchange words
-// through ds_bpermute.  The table level is clamp(rint(c * s)) with the rounding done by adding 1.5 * 2^23 (the sum
-// is an integer in [2^23, 2^24), its low byte the two's-complement level).
+// v_mfma_i32_16x16x64_i8 takes 16 rows of A per fragment, so one A fragment feeds the two 16-column groups of a
+// wavefront's 32 columns.  A super-step is 128 k: lane group g = lane / 16 takes the 32 consecutive k
+// [128t + 32g, 128t + 32g + 32) of its column and splits them over the two MFMA sub-steps (k + [0, 16), k + [16, 32));
+// its A fragments take the same k of its row (any permutation of k applied to both operands leaves the sums
+// unchanged).  So the four lanes of a column share a scale wherever the group spans 128 k (64: pairs of lanes): each
+// builds one word (two) of the 16-byte table and they exchange words through ds_bpermute.  The table level is
+// clamp(rint(c * s)) with the rounding done by adding 1.5 * 2^23 (the sum is an integer in [2^23, 2^24), its low
+// byte the two's-complement level).
 //
-// A workgroup of 8 wavefronts owns 32 columns; the wavefronts split K in eight and meet in LDS (fixed order).
-// Loads go through buffer descriptors: one 32-bit lane offset per operand, the step in the scalar offset, so the
-// K loop spends no VALU on addresses.  Chunks of kC16Chunk super-steps are double-buffered in registers.
-constexpr int kC16Waves = 8;
-constexpr int kSS = 128;        // k per super-step
-constexpr int kC16Chunk = 2;    // super-steps per register chunk
+// Loads.  A workgroup owns 32 columns; its wavefronts split K into contiguous runs of stages (256 k).  A wavefront
+// stages its packed weight (32 columns x 128 bytes) and A (16 rows x 256 bytes) in 8 KiB of LDS, loaded as whole
+// 128-byte lines (8 lanes per line) through a buffer descriptor, then reads its MFMA fragments back with
+// ds_read_b128: the fragment layout touches each line in 64-byte halves, which costs twice the memory requests when
+// loaded straight into registers.  The next stage's loads (32 registers per lane) are in flight while this stage
+// computes; they go to LDS after its fragment reads.  The lane offsets are fixed; the stage moves in the scalar
+// offset.  The wavefronts' partial sums meet in LDS in a fixed order.
+constexpr int kSS = 128;           // k per super-step
 constexpr int kC16MinTiles = 128;  // fewer 32-column tiles leave the chip idle: the split-K column kernel serves
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
@@ -422,150 +425,60 @@ __device__ __forceinline__ uint32_t lut_word(const float* c, float s, bool fast)
   return level(c[0], s) | (level(c[1], s) << 8) | (level(c[2], s) << 16) | (level(c[3], s) << 24);
 }
 
-template <int MR, int GK>
-struct C16Chunk {
-  u32x4 pq[kC16Chunk][2];              // [super-step][column group]: 32 packed k of the lane's column
-  u32x4 pa[kC16Chunk][MR][2];          // [super-step][row group][sub-step]: 16 k of the lane's row
-  uint32_t s[kC16Chunk][2][GK == 16 ? 2 : 1];  // raw scale bits [super-step][column group][16-k half]
-};
+// LDS staging of one wavefront: kStage k of its 32 columns (packed) and of the 16 A rows.  A 16-byte chunk of column
+// c (row r) sits at chunk index ch ^ ((c >> 1) & 7) (ch ^ r), so the 16 lanes of one ds_read_b128 pass (same lane
+// group, 16 columns or rows) hit 16 different bank groups; the loads choose their global chunk to match.
+constexpr int kStage = 256;                  // k per stage: two super-steps, whole 128-byte lines of packed weight
+constexpr int kQStage = 32 * kStage / 2;     // 4 KiB
+constexpr int kAStage = 16 * kStage;         // 4 KiB
+constexpr int kWaveLds = kQStage + kAStage;
+constexpr int kC16MaxWaves = 8;              // <= 128 VGPRs: two workgroups of 8 per CU (64 KiB of LDS each)
 
-struct C16Lanes {
-  rsrc_t rq, ra, rs;
-  uint32_t qv[2];   // byte offsets of the lane's packed k in its two columns
-  uint32_t av[2];   // byte offsets of the lane's k in its row of each row group
-  uint32_t sv[2];   // byte offsets of the lane's first scale in its two columns
-};
-
-// Super-steps first .. first + kC16Chunk - 1 of the wavefront's range (ss0 + ..); slots past nss reload the last
-// valid super-step and are not computed.
-template <int MR, int SD, int GK>
-__device__ __forceinline__ void c16_load(C16Chunk<MR, GK>& c, int first, int nss, int ss0, const C16Lanes& L,
-                                         int group) {
+template <int SD, int GK>
+__global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
+    const int8_t* __restrict__ A, int64_t lda, const float* __restrict__ xs, const uint8_t* __restrict__ q, int64_t ldq,
+    const void* __restrict__ s_rel, int64_t lds, const float* __restrict__ cb, int group, const float* __restrict__ sch,
+    const void* __restrict__ bias, int M, int N, int K, int spw, void* __restrict__ out, int64_t ldo, int odt,
+    bool eager, int32_t* __restrict__ acc_out) {
+  __shared__ __attribute__((aligned(1024))) int8_t smem[kC16MaxWaves * kWaveLds];
   constexpr uint32_t sb = scale_bytes<SD>();
-#pragma unroll
-  for (int j = 0; j < kC16Chunk; ++j) {
-    const int ss = ss0 + min(first + j, nss - 1);
-#pragma unroll
-    for (int cg = 0; cg < 2; ++cg) c.pq[j][cg] = bload16(L.rq, L.qv[cg], static_cast<uint32_t>(ss) * (kSS / 2));
-#pragma unroll
-    for (int r = 0; r < MR; ++r)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) c.pa[j][r][s] = bload16(L.ra, L.av[r] + s * 16, static_cast<uint32_t>(ss) * kSS);
-    uint32_t sidx;  // uniform part of the scale index
-    if (GK == 128) sidx = static_cast<uint32_t>(ss * kSS / group);
-    else sidx = static_cast<uint32_t>(ss) * (kSS / GK);
-#pragma unroll
-    for (int cg = 0; cg < 2; ++cg) {
-      c.s[j][cg][0] = bload_scale_bits<SD>(L.rs, L.sv[cg], sidx * sb);
-      if (GK == 16) c.s[j][cg][GK == 16 ? 1 : 0] = bload_scale_bits<SD>(L.rs, L.sv[cg] + sb, sidx * sb);
-    }
-  }
-}
-
-template <int MR, int SD, int GK, int NCB>
-__device__ __forceinline__ void c16_compute(const C16Chunk<MR, GK>& c, int first, int nss, int ss0,
-                                            const float (&cbw)[NCB], bool cbw_finite, const uint32_t (&bp)[2],
-                                            uint32_t (&lut)[2][4], uint32_t (&lut2)[2][4], v4i (&acc)[MR][2],
-                                            int group) {
-#pragma unroll
-  for (int j = 0; j < kC16Chunk; ++j) {
-    const int i = first + j;
-    if (i >= nss) break;  // uniform
-    const int ss = ss0 + i;
-    const bool rebuild = GK != 128 || i == 0 || (ss * kSS) % group == 0;  // uniform
-    if (rebuild) {
-#pragma unroll
-      for (int cg = 0; cg < 2; ++cg) {
-        const float s = scale_value<SD>(c.s[j][cg][0]);
-        const bool fast = cbw_finite && __builtin_isfinite(s);
-        if (GK == 128) {  // this lane built word g; word w comes from lane group w of the column
-          const uint32_t x = lut_word(&cbw[0], s, fast);
-#pragma unroll
-          for (int w = 0; w < 4; ++w)
-            lut[cg][w] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp[0] + 64 * w),
-                                                                            static_cast<int>(x)));
-        } else if (GK == 64) {  // this lane built words 2h, 2h + 1 (h = g & 1); the pair is lane groups g & 2, +1
-          const uint32_t x0 = lut_word(&cbw[0], s, fast), x1 = lut_word(&cbw[4], s, fast);
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            lut[cg][2 * h] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp[h]), static_cast<int>(x0)));
-            lut[cg][2 * h + 1] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp[h]), static_cast<int>(x1)));
-          }
-        } else {
-#pragma unroll
-          for (int w = 0; w < 4; ++w) lut[cg][w] = lut_word(&cbw[4 * w], s, fast);
-          if (GK == 16) {
-            const float s2 = scale_value<SD>(c.s[j][cg][GK == 16 ? 1 : 0]);
-            const bool fast2 = cbw_finite && __builtin_isfinite(s2);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) lut2[cg][w] = lut_word(&cbw[4 * w], s2, fast2);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int cg = 0; cg < 2; ++cg) {
-      v4i bf[2];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        uint32_t lo4, hi4;
-        if (GK == 16 && w >= 2) lut_decode_word(lut2[cg], c.pq[j][cg][w], lo4, hi4);
-        else lut_decode_word(lut[cg], c.pq[j][cg][w], lo4, hi4);
-        bf[w >> 1][(w & 1) * 2] = static_cast<int>(lo4);
-        bf[w >> 1][(w & 1) * 2 + 1] = static_cast<int>(hi4);
-      }
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          const u32x4 a = c.pa[j][r][s];
-          const v4i af = {static_cast<int>(a[0]), static_cast<int>(a[1]), static_cast<int>(a[2]), static_cast<int>(a[3])};
-          acc[r][cg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[s], acc[r][cg], 0, 0, 0);
-        }
-    }
-  }
-}
-
-template <int MR, int SD, int GK>
-__global__ __launch_bounds__(512) void gemm_w4_c16_kernel(const int8_t* __restrict__ A, int64_t lda,
-                                                          const float* __restrict__ xs, const uint8_t* __restrict__ q,
-                                                          int64_t ldq, const void* __restrict__ s_rel, int64_t lds,
-                                                          const float* __restrict__ cb, int group,
-                                                          const float* __restrict__ sch, const void* __restrict__ bias,
-                                                          int M, int N, int K, int wss, void* __restrict__ out,
-                                                          int64_t ldo, int odt, bool eager,
-                                                          int32_t* __restrict__ acc_out) {
-  constexpr int R = MR * 8;  // accumulator registers per lane
-  __shared__ int32_t red[kC16Waves][R][64];
-  constexpr uint32_t sb = scale_bytes<SD>();
+  constexpr int NS = GK == 16 ? 2 : 1;  // scales per lane, column and super-step
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = static_cast<int>(blockDim.x) >> 6;
   const int g = lane >> 4, c16 = lane & 15;
-  const int KS = K / kSS;
-  const int ss0 = wave * wss;
-  const int nss = max(0, min(wss, KS - ss0));
+  const int KS = K / kSS, NSTG = (KS + 1) / 2;
+  const int st0 = wave * spw;
+  const int nst = max(0, min(spw, NSTG - st0));
+  int8_t* const qs = smem + wave * kWaveLds;  // the wavefront's stage: packed weight, then A
+  int8_t* const as = qs + kQStage;
 
-  C16Lanes L;
-  L.rq = make_rsrc(q, static_cast<uint32_t>(static_cast<int64_t>(N - 1) * ldq + K / 2));
-  L.ra = make_rsrc(A, static_cast<uint32_t>(static_cast<int64_t>(M - 1) * lda + K));
-  L.rs = make_rsrc(s_rel, static_cast<uint32_t>((static_cast<int64_t>(N - 1) * lds + K / group) * sb));
+  const rsrc_t rq = make_rsrc(q, static_cast<uint32_t>(static_cast<int64_t>(N - 1) * ldq + K / 2));
+  const rsrc_t ra = make_rsrc(A, static_cast<uint32_t>(static_cast<int64_t>(M - 1) * lda + K));
+  const rsrc_t rs = make_rsrc(s_rel, static_cast<uint32_t>((static_cast<int64_t>(N - 1) * lds + K / group) * sb));
+  // load i: packed-weight columns 8i + lane / 8 (8 lanes per 128-byte line), A rows 4i + lane / 16 (16 lanes per
+  // 256-byte row); each lane's 16 bytes go to their swizzled LDS chunk.  Columns past N and rows past M are not
+  // clamped: their offsets lie past the descriptor's range, the loads return zeros, and those columns and rows only
+  // reach outputs that are never stored.
+  const uint32_t qoff = static_cast<uint32_t>((static_cast<int64_t>(blockIdx.x) * 32 + (lane >> 3)) * ldq + ((lane & 7) << 4));
+  const uint32_t aoff = static_cast<uint32_t>(static_cast<int64_t>(lane >> 4) * lda + ((lane & 15) << 4));
+  const uint32_t qstep = static_cast<uint32_t>(8 * ldq), astep = static_cast<uint32_t>(4 * lda);  // per load i
+  // LDS chunk of load i: q column c = 8i + lane / 8 at c * 128 + ((lane & 7) ^ ((c >> 1) & 7)) * 16, where
+  // (c >> 1) & 7 = 4 (i & 1) + lane / 16; A row r = 4i + lane / 16 at r * 256 + ((lane & 15) ^ r) * 16
+  const uint32_t qdst0 = static_cast<uint32_t>((lane >> 3) * 128 + (((lane & 7) ^ (lane >> 4)) << 4));
+  const uint32_t qdst1 = static_cast<uint32_t>((lane >> 3) * 128 + (((lane & 7) ^ (4 + (lane >> 4))) << 4));
+  const uint32_t adst0 = static_cast<uint32_t>((lane >> 4) * 256 + (((lane & 15) ^ (lane >> 4)) << 4));
+  uint32_t soff[2];  // the lane's first scale of its two columns (past N: past the range, zeros)
 #pragma unroll
   for (int cg = 0; cg < 2; ++cg) {
-    const int col = min(blockIdx.x * 32 + cg * 16 + c16, N - 1);
-    L.qv[cg] = static_cast<uint32_t>(static_cast<int64_t>(col) * ldq + g * 16);
-    uint32_t sl = 0;  // the lane's part of the scale index
+    const int col = static_cast<int>(blockIdx.x) * 32 + cg * 16 + c16;
+    uint32_t sl = 0;
     if (GK == 64) sl = g >> 1;
     else if (GK == 32) sl = g;
     else if (GK == 16) sl = 2 * g;
-    L.sv[cg] = static_cast<uint32_t>((static_cast<int64_t>(col) * lds + sl) * sb);
+    soff[cg] = static_cast<uint32_t>((static_cast<int64_t>(col) * lds + sl) * sb);
   }
-#pragma unroll
-  for (int r = 0; r < MR; ++r) {
-    const int row = min(r * 16 + c16, M - 1);
-    L.av[r] = static_cast<uint32_t>(static_cast<int64_t>(row) * lda + g * 32);
-  }
-  if (MR == 1) L.av[1] = L.av[0];  // unused
 
   constexpr int NCB = GK == 128 ? 4 : (GK == 64 ? 8 : 16);
   float cbw[NCB];
@@ -575,48 +488,133 @@ __global__ __launch_bounds__(512) void gemm_w4_c16_kernel(const int8_t* __restri
   bool cbw_finite = true;
 #pragma unroll
   for (int i = 0; i < NCB; ++i) cbw_finite = cbw_finite && __builtin_isfinite(cbw[i]);
-  uint32_t bp[2];  // ds_bpermute byte addresses of the column's table builders
-  if (GK == 128) {
-    bp[0] = static_cast<uint32_t>(c16 * 4);
-    bp[1] = 0;
-  } else {
-    bp[0] = static_cast<uint32_t>((c16 + 16 * (g & 2)) * 4);
-    bp[1] = bp[0] + 64;
-  }
+  // ds_bpermute byte addresses of the lanes that build the column's table words
+  const uint32_t bp0 = GK == 128 ? static_cast<uint32_t>(c16 * 4) : static_cast<uint32_t>((c16 + 16 * (g & 2)) * 4);
 
-  v4i acc[MR][2];
-#pragma unroll
-  for (int r = 0; r < MR; ++r) acc[r][0] = acc[r][1] = v4i{0, 0, 0, 0};
+  v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
   uint32_t lut[2][4] = {}, lut2[2][4] = {};
 
-  C16Chunk<MR, GK> c0, c1;
-  if (nss > 0) c16_load<MR, SD, GK>(c0, 0, nss, ss0, L, group);
-  for (int first = 0; first < nss; first += 2 * kC16Chunk) {
-    if (first + kC16Chunk < nss) c16_load<MR, SD, GK>(c1, first + kC16Chunk, nss, ss0, L, group);
-    c16_compute<MR, SD, GK>(c0, first, nss, ss0, cbw, cbw_finite, bp, lut, lut2, acc, group);
-    if (first + 2 * kC16Chunk < nss) c16_load<MR, SD, GK>(c0, first + 2 * kC16Chunk, nss, ss0, L, group);
-    c16_compute<MR, SD, GK>(c1, first + kC16Chunk, nss, ss0, cbw, cbw_finite, bp, lut, lut2, acc, group);
+  // ---- stage st into registers (whole-line loads) and the scales of its super-steps
+  u32x4 rq4[4], ra4[4];
+  uint32_t snext[2][2][NS], scur[2][2][NS];  // [super-step][column group][16-k half]
+  auto load = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rq4[i] = bload16(rq, qoff, static_cast<uint32_t>(st) * (kStage / 2) + i * qstep);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra4[i] = bload16(ra, aoff, static_cast<uint32_t>(st) * kStage + i * astep);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ss = min(2 * st + j, KS - 1);
+      const uint32_t sidx = GK == 128 ? static_cast<uint32_t>(ss * kSS / group) : static_cast<uint32_t>(ss) * (kSS / GK);
+#pragma unroll
+      for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+        for (int h = 0; h < NS; ++h) snext[j][cg][h] = bload_scale_bits<SD>(rs, soff[cg] + h * sb, sidx * sb);
+    }
+  };
+  // ---- registers -> the wavefront's LDS stage (a wavefront's LDS accesses execute in order: the previous stage's
+  // fragment reads are done before these writes land)
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(qs + 1024 * i + ((i & 1) ? qdst1 : qdst0)) = rq4[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(as + 1024 * i + (adst0 ^ (i << 6))) = ra4[i];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+        for (int h = 0; h < NS; ++h) scur[j][cg][h] = snext[j][cg][h];
+  };
+  // ---- compute stage st (the t-th of the wavefront)
+  auto compute = [&](int t, int st) {
+    const int nss = 2 * st + 1 < KS ? 2 : 1;  // uniform
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (j >= nss) break;
+      const int ss = 2 * st + j;
+      const bool rebuild = GK != 128 || (t == 0 && j == 0) || (ss * kSS) % group == 0;  // uniform
+      if (rebuild) {
+#pragma unroll
+        for (int cg = 0; cg < 2; ++cg) {
+          const float s = scale_value<SD>(scur[j][cg][0]);
+          const bool fast = cbw_finite && __builtin_isfinite(s);
+          if (GK == 128) {  // this lane built word g; word w comes from lane group w of the column
+            const uint32_t x = lut_word(&cbw[0], s, fast);
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+              lut[cg][w] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp0 + 64 * w),
+                                                                              static_cast<int>(x)));
+          } else if (GK == 64) {  // words 2h, 2h + 1 (h = g & 1); the pair is lane groups g & 2 and (g & 2) + 1
+            const uint32_t x0 = lut_word(&cbw[0], s, fast), x1 = lut_word(&cbw[4], s, fast);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              lut[cg][2 * h] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp0 + 64 * h),
+                                                                                  static_cast<int>(x0)));
+              lut[cg][2 * h + 1] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp0 + 64 * h),
+                                                                                      static_cast<int>(x1)));
+            }
+          } else {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) lut[cg][w] = lut_word(&cbw[4 * w], s, fast);
+            if (GK == 16) {
+              const float s2 = scale_value<SD>(scur[j][cg][NS - 1]);
+              const bool fast2 = cbw_finite && __builtin_isfinite(s2);
+#pragma unroll
+              for (int w = 0; w < 4; ++w) lut2[cg][w] = lut_word(&cbw[4 * w], s2, fast2);
+            }
+          }
+        }
+      }
+      v4i af[2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+        af[sub] = *reinterpret_cast<const v4i*>(as + c16 * 256 + (((j * 8 + g * 2 + sub) ^ c16) << 4));
+#pragma unroll
+      for (int cg = 0; cg < 2; ++cg) {
+        const int c = cg * 16 + c16;
+        const u32x4 pk = *reinterpret_cast<const u32x4*>(qs + c * 128 + (((4 * j + g) ^ ((c >> 1) & 7)) << 4));
+        v4i bf[2];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t lo4, hi4;
+          if (GK == 16 && w >= 2) lut_decode_word(lut2[cg], pk[w], lo4, hi4);
+          else lut_decode_word(lut[cg], pk[w], lo4, hi4);
+          bf[w >> 1][(w & 1) * 2] = static_cast<int>(lo4);
+          bf[w >> 1][(w & 1) * 2 + 1] = static_cast<int>(hi4);
+        }
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) acc[cg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[sub], bf[sub], acc[cg], 0, 0, 0);
+      }
+    }
+  };
+  // ---- the next stage loads while this one computes
+  if (nst > 0) {
+    load(st0);
+    store();
+  }
+  for (int t = 0; t < nst; ++t) {
+    if (t + 1 < nst) load(st0 + t + 1);
+    compute(t, st0 + t);
+    if (t + 1 < nst) store();
   }
 
-#pragma unroll
-  for (int r = 0; r < MR; ++r)
-#pragma unroll
-    for (int cg = 0; cg < 2; ++cg)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[wave][(r * 2 + cg) * 4 + i][lane] = acc[r][cg][i];
+  // ---- the wavefronts' partial sums meet in LDS (the staging area, now free), fixed order
+  int32_t* const red = reinterpret_cast<int32_t*>(smem);  // [wave][8 registers][64 lanes]
   __syncthreads();
-  // wavefront w finishes registers [w * MR, (w + 1) * MR) of every lane; C of 16x16: lane -> column lane % 16,
-  // register i -> row 4 * (lane / 16) + i
 #pragma unroll
-  for (int u = 0; u < R / kC16Waves; ++u) {
-    const int rr = wave * (R / kC16Waves) + u;
-    const int r = rr >> 3, cg = (rr >> 2) & 1, i = rr & 3;
-    const int m = r * 16 + g * 4 + i;
-    const int col = blockIdx.x * 32 + cg * 16 + c16;
+  for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 8 + cg * 4 + i) * 64 + lane] = acc[cg][i];
+  __syncthreads();
+  // register rr of lane l: column group rr / 4, row 4 * (l / 16) + rr % 4, column l % 16 (16x16 C layout)
+  for (int rr = wave; rr < 8; rr += nw) {
+    const int cg = rr >> 2, i = rr & 3;
+    const int m = g * 4 + i;
+    const int col = static_cast<int>(blockIdx.x) * 32 + cg * 16 + c16;
     if (m >= M || col >= N) continue;
     int a = 0;
-#pragma unroll
-    for (int w = 0; w < kC16Waves; ++w) a += red[w][rr][lane];
+    for (int w = 0; w < nw; ++w) a += red[(w * 8 + rr) * 64 + lane];
     const int64_t e = static_cast<int64_t>(m) * N + col;
     if (acc_out) acc_out[e] = a;
     store_out(odt, eager, a, xs[m], sch[col], bias ? load_bias(odt, bias, col) : 0.0f, bias != nullptr, out,
@@ -722,29 +720,23 @@ inline bool c16_ok(int64_t m, int64_t n, int64_t k, int group, int64_t lda, int6
          ((n - 1) * lds + k / group) * sbytes <= lim;
 }
 
-template <int MR, int SD>
-void launch_c16_g(int mode, int odt, const int8_t* a, int64_t lda, const float* xs, const uint8_t* q, int64_t ldq,
-                  const void* s_rel, int64_t lds, const float* cb, int group, const float* sch, const void* bias, int m,
-                  int n, int k, void* out, int64_t ldo, int32_t* acc_out, hipStream_t st) {
+template <int SD>
+void launch_c16(int mode, int odt, const int8_t* a, int64_t lda, const float* xs, const uint8_t* q, int64_t ldq,
+                const void* s_rel, int64_t lds, const float* cb, int group, const float* sch, const void* bias, int m,
+                int n, int k, void* out, int64_t ldo, int32_t* acc_out, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>((n + 31) / 32));
-  const int ks = k / kSS;
-  const int wss = (ks + kC16Waves - 1) / kC16Waves;
+  const int nstg = (k / kSS + 1) / 2;
+  const int spw = (nstg + kC16MaxWaves - 1) / kC16MaxWaves;  // stages per wavefront
+  const int nw = (nstg + spw - 1) / spw;                       // wavefronts per workgroup, <= kC16MaxWaves
   const bool eager = mode == H3K_MODE_EAGER;
-#define H3K_C16(GK)                                                                                              \
-  hipLaunchKernelGGL((gemm_w4_c16_kernel<MR, SD, GK>), grid, dim3(64 * kC16Waves), 0, st, a, lda, xs, q, ldq, s_rel, \
-                     lds, cb, group, sch, bias, m, n, k, wss, out, ldo, odt, eager, acc_out)
+#define H3K_C16(GK)                                                                                                  \
+  hipLaunchKernelGGL((gemm_w4_c16_kernel<SD, GK>), grid, dim3(64 * nw), 0, st, a, lda, xs, q, ldq, s_rel, lds, cb,  \
+                     group, sch, bias, m, n, k, spw, out, ldo, odt, eager, acc_out)
   if (group == 16) H3K_C16(16);
   else if (group == 32) H3K_C16(32);
   else if (group == 64) H3K_C16(64);
   else H3K_C16(128);
 #undef H3K_C16
-}
-
-template <int SD>
-void launch_c16(int mode, int odt, const int8_t* a, int64_t lda, const float* xs, const uint8_t* q, int64_t ldq,
-                const void* s_rel, int64_t lds, const float* cb, int group, const float* sch, const void* bias, int m,
-                int n, int k, void* out, int64_t ldo, int32_t* acc_out, hipStream_t st) {
-  launch_c16_g<1, SD>(mode, odt, a, lda, xs, q, ldq, s_rel, lds, cb, group, sch, bias, m, n, k, out, ldo, acc_out, st);
 }
 
 template <int MB, int SD>
