@@ -434,6 +434,7 @@ constexpr int kAStage = 16 * kStage;         // 4 KiB
 constexpr int kWaveLds = kQStage + kAStage;
 constexpr int kC16MaxWaves = 8;              // <= 128 VGPRs: two workgroups of 8 per CU (64 KiB of LDS each)
 
+// GK: 16, 32, 64, 128 (group 128) or 256 (a multiple of 128 above 128: the table is rebuilt where a group starts)
 template <int SD, int GK>
 __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
     const int8_t* __restrict__ A, int64_t lda, const float* __restrict__ xs, const uint8_t* __restrict__ q, int64_t ldq,
@@ -480,16 +481,16 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
     soff[cg] = static_cast<uint32_t>((static_cast<int64_t>(col) * lds + sl) * sb);
   }
 
-  constexpr int NCB = GK == 128 ? 4 : (GK == 64 ? 8 : 16);
+  constexpr int NCB = GK >= 128 ? 4 : (GK == 64 ? 8 : 16);
   float cbw[NCB];
-  const int cb0 = GK == 128 ? 4 * g : (GK == 64 ? 8 * (g & 1) : 0);
+  const int cb0 = GK >= 128 ? 4 * g : (GK == 64 ? 8 * (g & 1) : 0);
 #pragma unroll
   for (int i = 0; i < NCB; ++i) cbw[i] = cb[cb0 + i];
   bool cbw_finite = true;
 #pragma unroll
   for (int i = 0; i < NCB; ++i) cbw_finite = cbw_finite && __builtin_isfinite(cbw[i]);
   // ds_bpermute byte addresses of the lanes that build the column's table words
-  const uint32_t bp0 = GK == 128 ? static_cast<uint32_t>(c16 * 4) : static_cast<uint32_t>((c16 + 16 * (g & 2)) * 4);
+  const uint32_t bp0 = GK >= 128 ? static_cast<uint32_t>(c16 * 4) : static_cast<uint32_t>((c16 + 16 * (g & 2)) * 4);
 
   v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
   uint32_t lut[2][4] = {}, lut2[2][4] = {};
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ss = min(2 * st + j, KS - 1);
-      const uint32_t sidx = GK == 128 ? static_cast<uint32_t>(ss * kSS / group) : static_cast<uint32_t>(ss) * (kSS / GK);
+      const uint32_t sidx = GK >= 128 ? static_cast<uint32_t>(ss * kSS / group) : static_cast<uint32_t>(ss) * (kSS / GK);
 #pragma unroll
       for (int cg = 0; cg < 2; ++cg)
 #pragma unroll
@@ -527,19 +528,21 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
         for (int h = 0; h < NS; ++h) scur[j][cg][h] = snext[j][cg][h];
   };
   // ---- compute stage st (the t-th of the wavefront)
-  auto compute = [&](int t, int st) {
-    const int nss = 2 * st + 1 < KS ? 2 : 1;  // uniform
+  // NSS super-steps (2, or 1 for a last half stage); FAST: the codebook and every scale of the stage are finite in
+  // all lanes (uniform), so the tables take the branch-free form and the stage is straight-line code
+  auto compute = [&](auto nc, auto fc, int t, int st) {
+    constexpr int NSS = decltype(nc)::value;
+    constexpr bool FAST = decltype(fc)::value;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (j >= nss) break;
+    for (int j = 0; j < NSS; ++j) {
       const int ss = 2 * st + j;
-      const bool rebuild = GK != 128 || (t == 0 && j == 0) || (ss * kSS) % group == 0;  // uniform
+      const bool rebuild = GK != 256 || (t == 0 && j == 0) || (ss * kSS) % group == 0;  // uniform
       if (rebuild) {
 #pragma unroll
         for (int cg = 0; cg < 2; ++cg) {
           const float s = scale_value<SD>(scur[j][cg][0]);
-          const bool fast = cbw_finite && __builtin_isfinite(s);
-          if (GK == 128) {  // this lane built word g; word w comes from lane group w of the column
+          const bool fast = FAST || (cbw_finite && __builtin_isfinite(s));
+          if (GK >= 128) {  // this lane built word g; word w comes from lane group w of the column
             const uint32_t x = lut_word(&cbw[0], s, fast);
 #pragma unroll
             for (int w = 0; w < 4; ++w)
@@ -559,7 +562,7 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
             for (int w = 0; w < 4; ++w) lut[cg][w] = lut_word(&cbw[4 * w], s, fast);
             if (GK == 16) {
               const float s2 = scale_value<SD>(scur[j][cg][NS - 1]);
-              const bool fast2 = cbw_finite && __builtin_isfinite(s2);
+              const bool fast2 = FAST || (cbw_finite && __builtin_isfinite(s2));
 #pragma unroll
               for (int w = 0; w < 4; ++w) lut2[cg][w] = lut_word(&cbw[4 * w], s2, fast2);
             }
@@ -595,7 +598,27 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
   }
   for (int t = 0; t < nst; ++t) {
     if (t + 1 < nst) load(st0 + t + 1);
-    compute(t, st0 + t);
+    {
+      const int st = st0 + t;
+      bool fin = cbw_finite;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+          for (int h = 0; h < NS; ++h) fin = fin && __builtin_isfinite(scale_value<SD>(scur[j][cg][h]));
+      const bool all_fin = GK >= 64 && __builtin_amdgcn_ballot_w64(!fin) == 0;  // uniform
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using T = std::true_type;
+      using F = std::false_type;
+      if (2 * st + 1 < KS) {
+        if (GK >= 64 && all_fin) compute(I2{}, T{}, t, st);  // (groups 16 / 32: past 128 VGPRs)
+        else compute(I2{}, F{}, t, st);
+      } else {
+        compute(I1{}, F{}, t, st);
+      }
+    }
     if (t + 1 < nst) store();
   }
 
@@ -735,7 +758,8 @@ void launch_c16(int mode, int odt, const int8_t* a, int64_t lda, const float* xs
   if (group == 16) H3K_C16(16);
   else if (group == 32) H3K_C16(32);
   else if (group == 64) H3K_C16(64);
-  else H3K_C16(128);
+  else if (group == 128) H3K_C16(128);
+  else H3K_C16(256);
 #undef H3K_C16
 }
 
