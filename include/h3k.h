@@ -103,7 +103,7 @@ int h3k_gemm_w4a8(const int8_t* a, int64_t lda, const float* xs, const void* q, 
                   int32_t* acc_out, void* stream);
 
 /*
- * The whole W4A8 ConvRot linear: rotate+quantise x, decode the weight, GEMM + epilogue (m <= 128 with k a multiple
+ * The whole W4A8 ConvRot linear: rotate+quantise x, decode the weight, GEMM + epilogue (m <= 64 with k a multiple
  * of 64: the fused few-row GEMM, no decode pass).
  * Fills the slot of comfy_kitchen's w4a8_int8_linear call, h3turbo/h3/qlinear.py:427-429 (_run_ck).
  * workspace: device scratch of at least h3k_w4a8_linear_workspace(m, n, k) bytes, 256-byte aligned.

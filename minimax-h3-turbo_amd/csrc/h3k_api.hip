@@ -51,8 +51,9 @@ static size_t weight_region(int64_t m, int64_t n, int64_t k) {
   return grid > acc ? grid : acc;
 }
 
+// Chunks of up to 64 rows take the fused int4 GEMM; from ~100 rows the decode + int8 GEMM pair is faster.
 static bool fused_few_rows(int64_t m, int64_t k, int group, const void* q, int64_t ldq) {
-  return m <= 128 && k % 64 == 0 && (group == 16 || group == 32 || (group > 0 && group % 64 == 0)) && k % group == 0 &&
+  return m <= 64 && k % 64 == 0 && (group == 16 || group == 32 || (group > 0 && group % 64 == 0)) && k % group == 0 &&
          aligned(q, 16) && ldq % 16 == 0;
 }
 

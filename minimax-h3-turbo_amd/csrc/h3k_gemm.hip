@@ -210,8 +210,10 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
     gemm_pipe_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
   else if (m >= 2048 && n >= 256)
     launch_gemm_dt<4, 4>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
-  else
+  else if (((m + 127) / 128) * ((n + 127) / 128) >= 256)
     launch_gemm_dt<2, 2>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
+  else  // fewer 128 x 128 tiles than CUs: 64 x 64 tiles (M=512: N=5120 451 -> 630 TOPS, K=13824 559 -> 738)
+    launch_gemm_dt<1, 1>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
   return check_launch("gemm_a8w8");
 }
 

@@ -1,4 +1,4 @@
-"""The large-shape GEMM kernels (persistent and pipelined, chosen by shape and alignment) against the CPU oracle
+"""The GEMM kernels (persistent and pipelined for large M; 64 x 64 or 128 x 128 tiles for small M) against the CPU oracle
 on whole outputs: ragged M and N tails, K-step counts that do not divide the pipeline depth, every epilogue
 variant (ck / eager, bf16 / f16 / f32 out, bias, the int32 accumulator dump, unaligned output strides), and grids
 where every persistent workgroup walks several tiles (full tiles only, and full tiles mixed with cut ones).
@@ -52,6 +52,19 @@ def test_large_kernels_ragged_shapes_bf16(m, n, k):
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_large_kernels_every_epilogue(mode, odt, with_bias):
     run(1100, 520, 640, mode, odt, with_bias, seed=3)
+
+
+@pytest.mark.parametrize("m,n,k", [(200, 700, 320), (512, 5120, 576), (77, 130, 1040), (512, 8320, 256), (300, 16400, 128)])
+def test_small_m_kernel_tile_shapes(m, n, k):
+    # fewer than 256 tiles of 128 x 128: 64 x 64 tiles; otherwise 128 x 128 (ragged M and N in both)
+    run(m, n, k, "ck", _lib.BF16, False, seed=m + n)
+
+
+@pytest.mark.parametrize("mode", ["ck", "eager"])
+@pytest.mark.parametrize("odt", [_lib.BF16, _lib.F16, _lib.F32])
+def test_small_m_kernel_every_epilogue(mode, odt):
+    run(130, 600, 448, mode, odt, True, ldo_pad=8, acc=True, seed=3)  # 64 x 64 tiles
+    run(384, 11000, 192, mode, odt, True, ldo_pad=8, acc=True, seed=4)  # 128 x 128 tiles
 
 
 @pytest.mark.parametrize("m,n,k", [(6144, 8448, 512), (5000, 8000, 576)])
