@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
 
 #pragma unroll
   for (int p = 0; p < NPASS; ++p) {
-    const bool live = ((p * WPR + wr) * 4 + g) < nb;
+    // (blocks past the row hold zeros: their rotation is 0 and leaves the absmax alone)
     // (1) transpose the 16-bit input: lane l then holds elements l + 16*r, r = 0..15 (digits 2,3 local)
     wave_lds_sync();
     *reinterpret_cast<u32x4*>(tin + l * 16) = raw[p][0];
@@ -185,12 +185,10 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     for (int j = 0; j < 16; j += 2) {
       const float y0 = static_cast<float>(w[j]), y1 = static_cast<float>(w[j + 1]);
       const uint32_t b0 = round_bits_16<F16>(y0), b1 = round_bits_16<F16>(y1);
-      if (live) {
-        if (EAGER) {
-          amax = fmaxf(amax, fmaxf(fabsf(to_f32_16<F16>(b0)), fabsf(to_f32_16<F16>(b1))));
-        } else {
-          amax = fmaxf(amax, fmaxf(fabsf(y0), fabsf(y1)));
-        }
+      if (EAGER) {
+        amax = fmaxf(amax, fmaxf(fabsf(to_f32_16<F16>(b0)), fabsf(to_f32_16<F16>(b1))));
+      } else {
+        amax = fmaxf(amax, fmaxf(fabsf(y0), fabsf(y1)));
       }
       yb[p][j >> 1] = b0 | (b1 << 16);
     }
@@ -215,25 +213,45 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     const int b = (p * WPR + wr) * 4 + g;
     if (b >= nb) continue;
     uint32_t packed[4];
+    if (F16) {
 #pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4) {
-      uint32_t word = 0;
+      for (int w4 = 0; w4 < 4; ++w4) {
+        uint32_t word = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int j = w4 * 4 + e;
-        const uint32_t bits = (yb[p][j >> 1] >> ((j & 1) * 16)) & 0xFFFFu;
-        const float y = to_f32_16<F16>(bits);
-        float t;
-        if (F16) {
-          t = round_f16(fp32_round_point(y / s));
-        } else {
-          t = round_bf16(fp32_round_point(y * rs));
+        for (int e = 0; e < 4; ++e) {
+          const int j = w4 * 4 + e;
+          const float y = to_f32_16<F16>((yb[p][j >> 1] >> ((j & 1) * 16)) & 0xFFFFu);
+          float t = round_f16(fp32_round_point(y / s));
+          t = __builtin_rintf(t);
+          t = __builtin_amdgcn_fmed3f(t, -128.0f, 127.0f);
+          word |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xFFu) << (8 * e);
         }
-        t = __builtin_rintf(t);
-        t = __builtin_amdgcn_fmed3f(t, -128.0f, 127.0f);
-        word |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xFFu) << (8 * e);
+        packed[w4] = word;
       }
-      packed[w4] = word;
+    } else {
+      // Two elements per word: t = fl(y * fl(1/s)), one packed RNE conversion to bf16 for the pair, clamp, then
+      // rint by adding 1.5 * 2^23 (an integer in [2^23, 2^24): its low byte is the two's-complement level).
+      // Clamping before the rounding gives the same integer: the bounds are integers exact in bf16 and both
+      // roundings are monotone.  A NaN stays NaN through the clamp and the add, and its low byte is 0 (the low 16
+      // bits of a widened bf16 are 0), the level the integer conversion gives it.
+      uint32_t lv[16];
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const uint32_t wv = yb[p][h];
+        const float t0 = fp32_round_point(__uint_as_float(wv << 16) * rs);
+        const float t1 = fp32_round_point(__uint_as_float(wv & 0xFFFF0000u) * rs);
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const uint32_t tb = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){t0, t1}, bf16x2));
+        const float r0 = __builtin_amdgcn_fmed3f(__uint_as_float(tb << 16), -128.0f, 127.0f);
+        const float r1 = __builtin_amdgcn_fmed3f(__uint_as_float(tb & 0xFFFF0000u), -128.0f, 127.0f);
+        lv[2 * h] = __float_as_uint(fp32_round_point(r0 + 12582912.0f));
+        lv[2 * h + 1] = __float_as_uint(fp32_round_point(r1 + 12582912.0f));
+      }
+#pragma unroll
+      for (int w4 = 0; w4 < 4; ++w4)
+        packed[w4] = __builtin_amdgcn_perm(lv[4 * w4 + 1], lv[4 * w4], 0x0c0c0400u) |
+                     __builtin_amdgcn_perm(lv[4 * w4 + 3], lv[4 * w4 + 2], 0x04000c0cu);
     }
     __builtin_nontemporal_store(u32x4{packed[0], packed[1], packed[2], packed[3]},
                                 reinterpret_cast<u32x4*>(qr + b * 256 + l * 16));
