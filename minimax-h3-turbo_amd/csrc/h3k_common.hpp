@@ -88,6 +88,15 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// max that propagates NaN (IEEE 754-2019 maximum: v_maximum_f32 / v_maximum3_f32 on gfx950), like torch's amax
+__device__ __forceinline__ float nan_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+__device__ __forceinline__ float wave_nan_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = nan_max(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

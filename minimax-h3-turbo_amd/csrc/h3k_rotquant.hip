@@ -186,25 +186,28 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
       const float y0 = static_cast<float>(w[j]), y1 = static_cast<float>(w[j + 1]);
       const uint32_t b0 = round_bits_16<F16>(y0), b1 = round_bits_16<F16>(y1);
       if (EAGER) {
-        amax = fmaxf(amax, fmaxf(fabsf(to_f32_16<F16>(b0)), fabsf(to_f32_16<F16>(b1))));
+        amax = nan_max(amax, nan_max(fabsf(to_f32_16<F16>(b0)), fabsf(to_f32_16<F16>(b1))));
       } else {
-        amax = fmaxf(amax, fmaxf(fabsf(y0), fabsf(y1)));
+        amax = nan_max(amax, nan_max(fabsf(y0), fabsf(y1)));
       }
       yb[p][j >> 1] = b0 | (b1 << 16);
     }
   }
 
-  amax = wave_max(amax);
+  // NaN propagates through the absmax and the floor, as in torch's amax and clamp (a row holding inf or NaN)
+  amax = wave_nan_max(amax);
   if (WPR > 1) {
     if (lane == 0) s_amax[wave] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(s_amax[0], s_amax[1]), fmaxf(s_amax[2], s_amax[3]));
+    amax = nan_max(nan_max(s_amax[0], s_amax[1]), nan_max(s_amax[2], s_amax[3]));
   }
-  const float xsv = fmaxf(amax / 127.0f, 1e-30f);
+  const float xsv = nan_max(amax / 127.0f, 1e-30f);
+  const bool finite_row = __builtin_isfinite(amax);  // uniform: every y and the scale finite
   if (lane == 0 && wr == 0) xs[row] = xsv;
   float s = F16 ? round_f16(xsv) : round_bf16(xsv);
   if (s == 0.0f) s = F16 ? 6.103515625e-05f : 1.1754943508222875e-38f;
-  // bf16: bf16(y * fl(1/s)) == bf16(fl(y / s)) for bf16 y, s (8-bit mantissas; checked exhaustively on the CPU)
+  // bf16: bf16(y * fl(1/s)) == bf16(fl(y / s)) for bf16 y and every scale this kernel forms (>= bf16(1e-30));
+  // f16: the level is the same (both checked exhaustively on the CPU)
   const float rs = 1.0f / s;
 
   int8_t* qr = q + row * ldq;
@@ -213,7 +216,9 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     const int b = (p * WPR + wr) * 4 + g;
     if (b >= nb) continue;
     uint32_t packed[4];
-    if (F16) {
+    if (!finite_row) {
+      // a row with inf or NaN (rare): y * (1/s) is NaN where the reference's y / s is NaN (inf / inf, NaN), and a
+      // NaN quotient converts to level 0 (torch's and numpy's float -> int8 conversion on the reference's host)
 #pragma unroll
       for (int w4 = 0; w4 < 4; ++w4) {
         uint32_t word = 0;
@@ -221,13 +226,26 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
         for (int e = 0; e < 4; ++e) {
           const int j = w4 * 4 + e;
           const float y = to_f32_16<F16>((yb[p][j >> 1] >> ((j & 1) * 16)) & 0xFFFFu);
-          float t = round_f16(fp32_round_point(y / s));
-          t = __builtin_rintf(t);
-          t = __builtin_amdgcn_fmed3f(t, -128.0f, 127.0f);
-          word |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xFFu) << (8 * e);
+          const float t = round16<F16>(fp32_round_point(y * rs));
+          const float r = t != t ? 0.0f : __builtin_amdgcn_fmed3f(__builtin_rintf(t), -128.0f, 127.0f);
+          word |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xFFu) << (8 * e);
         }
         packed[w4] = word;
       }
+    } else if (F16) {
+      // f16: round_f16(fl(y * fl(1/s))) can differ from round_f16(fl(y / s)) only between f16 subnormals (|t| <
+      // 2^-14), never in the level (checked exhaustively on the CPU); clamp and rint as below.
+      uint32_t lv[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float y = to_f32_16<F16>((yb[p][j >> 1] >> ((j & 1) * 16)) & 0xFFFFu);
+        const float t = __builtin_amdgcn_fmed3f(round_f16(fp32_round_point(y * rs)), -128.0f, 127.0f);
+        lv[j] = __float_as_uint(fp32_round_point(t + 12582912.0f));
+      }
+#pragma unroll
+      for (int w4 = 0; w4 < 4; ++w4)
+        packed[w4] = __builtin_amdgcn_perm(lv[4 * w4 + 1], lv[4 * w4], 0x0c0c0400u) |
+                     __builtin_amdgcn_perm(lv[4 * w4 + 3], lv[4 * w4 + 2], 0x04000c0cu);
     } else {
       // Two elements per word: t = fl(y * fl(1/s)), one packed RNE conversion to bf16 for the pair, clamp, then
       // rint by adding 1.5 * 2^23 (an integer in [2^23, 2^24): its low byte is the two's-complement level).
@@ -300,7 +318,7 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
         const float y32 = static_cast<float>(buf[e] * scale);
         const float yr = round_dt<DT>(y32);
         if (sweep == 0) {
-          amax = fmaxf(amax, fabsf(EAGER ? yr : y32));
+          amax = nan_max(amax, fabsf(EAGER ? yr : y32));
         } else if (ROTATE_ONLY) {
           if (DT == H3K_F32) {
             static_cast<float*>(y)[row * ldy + c0 + e] = yr;
@@ -310,17 +328,17 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
           }
         } else {
           float tq = (DT == H3K_F32) ? (yr / s) : round_dt<DT>(fp32_round_point(yr / s));
-          tq = __builtin_amdgcn_fmed3f(__builtin_rintf(tq), -128.0f, 127.0f);
+          tq = tq != tq ? 0.0f : __builtin_amdgcn_fmed3f(__builtin_rintf(tq), -128.0f, 127.0f);  // NaN -> level 0
           q[row * ldq + c0 + e] = static_cast<int8_t>(static_cast<int>(tq));
         }
       }
     }
     if (sweep == 0) {
-      amax = wave_max(amax);
+      amax = wave_nan_max(amax);
       if ((t & 63) == 0) red[t >> 6] = amax;
       __syncthreads();
-      amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-      const float xsv = fmaxf(amax / 127.0f, 1e-30f);
+      amax = nan_max(nan_max(red[0], red[1]), nan_max(red[2], red[3]));
+      const float xsv = nan_max(amax / 127.0f, 1e-30f);
       if (t == 0) xs[row] = xsv;
       s = round_dt<DT>(xsv);
       if (s == 0.0f) s = DT == H3K_F16 ? 6.103515625e-05f : 1.1754943508222875e-38f;

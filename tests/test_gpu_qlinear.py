@@ -278,6 +278,53 @@ def test_rotation_sizes_and_dtypes_match_the_oracle(rot, dt):
     assert y.dtype == dt and np.array_equal(y.float().cpu().numpy(), yr)
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_rows_over_many_scales_match_the_oracle(dt):
+    """Row magnitudes from 1e-7 to 5e4 (f16: subnormal, tiny-clamped and large scales, the largest rows overflowing
+    to inf): the kernel's multiply by the reciprocal scale against the oracle's true division, bit for bit (NaN
+    scales of rows holding inf compare equal)."""
+    g = torch.Generator().manual_seed(77)
+    rows, k = 384, 1024
+    mag = torch.logspace(-7, 4.7, rows).unsqueeze(1)
+    x = (torch.randn(rows, k, generator=g) * mag).to(dt)
+    dts = {torch.bfloat16: "bf16", torch.float16: "f16"}[dt]
+    for mode in ("ck", "eager"):
+        q, s = ql.quantize_activation(x.to(DEV), quant_mode=mode)
+        qr, sr = ref.quantize_rows(x.float().numpy(), dts, 256, mode)
+        assert_scales(s.cpu().numpy(), sr, mode)
+        assert np.array_equal(q.cpu().numpy(), qr), mode
+
+
+def assert_scales(got, want, what):
+    """Finite scales bit for bit; where the reference scale is inf or NaN this one is the same or NaN (the s - 2x
+    butterfly turns a lone inf input into inf - inf) -- the row's levels are 0 and its linear output NaN either way."""
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin], want[fin]), what
+    assert (np.isnan(got[~fin]) | (got[~fin] == want[~fin])).all(), what
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_non_finite_rows_match_the_oracle(dt):
+    """A row holding one inf (every rotated value +-inf: reference scale inf, levels 0), +inf and -inf (inf - inf:
+    NaN), a NaN, a zero row and a finite one: scales NaN-propagating like torch's amax, NaN quotients at level 0."""
+    k = 512
+    x = torch.randn(6, k, generator=torch.Generator().manual_seed(5))
+    x[1, 7] = float("inf")
+    x[2, 3], x[2, 300] = float("inf"), float("-inf")
+    x[3, 100] = float("nan")
+    x[4] = 0.0
+    x[5, 9] = float("-inf")
+    x = x.to(dt)
+    dts = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[dt]
+    for mode in ("ck", "eager"):
+        q, s = ql.quantize_activation(x.to(DEV), quant_mode=mode)
+        qr, sr = ref.quantize_rows(x.float().numpy(), dts, 256, mode)
+        assert_scales(s.cpu().numpy(), sr, (mode, s.cpu().numpy().ravel(), sr.ravel()))
+        assert np.isfinite(sr[[0, 4, 5 - 5]]).all() and np.isnan(sr[3]).all()
+        assert np.array_equal(q.cpu().numpy(), qr), mode
+        assert not q[1:4].any()  # rows holding inf or NaN: every level 0
+
+
 def test_degenerate_rows():
     for dt in (torch.float32, torch.bfloat16, torch.float16):
         x = torch.zeros(4, 256, dtype=dt)
