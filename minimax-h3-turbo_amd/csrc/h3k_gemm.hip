@@ -11,7 +11,7 @@
 // the 16-byte global->LDS stores and the 16-byte MFMA fragment reads are bank-conflict free).  Operands that
 // fall outside M, N or K load as zeros; stores are masked.  Workgroup ids are remapped so each XCD works
 // through a contiguous, row-grouped range of tiles (its own L2 then serves the shared A/B panels).
-#include "h3k_common.hpp"
+#include "h3k_gemm_common.hpp"
 
 namespace h3k {
 
@@ -161,6 +161,28 @@ void gemm_persist_launch(const int8_t* a, int64_t lda, const float* xs, const in
                          const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo,
                          int32_t* acc_out, hipStream_t st);
 int gemm_persist_min_k();
+void gemm_pipe_mid_launch(int cfg, const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw,
+                          const float* s_ch, const void* bias, int m, int n, int k, int mode, void* out, int odt,
+                          int64_t ldo, int32_t* acc_out, hipStream_t st);
+int cu_count();
+
+#ifndef H3K_MID_FORCE
+#define H3K_MID_FORCE -1
+#endif
+
+
+// Tile shape of the mid-size pipeline launch: the largest tile that still gives at least 9/16 of the CUs a tile.
+// Measured at M = 64-512, K = 5120 / 13824, N = 5120-15360: 120 tiles of a shape lose to 240 of the next smaller
+// one, 160 win against 320.
+static int mid_tile(int m, int n) {
+  if (H3K_MID_FORCE >= 0) return H3K_MID_FORCE;
+  const int enough = cu_count() * 9 / 16;
+  auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+  if (tiles(128, 256) >= enough) return H3K_MID_128x256;
+  if (tiles(128, 128) >= enough) return H3K_MID_128x128;
+  if (tiles(64, 128) >= enough) return H3K_MID_64x128;
+  return H3K_MID_64x64;
+}
 
 #ifndef H3K_GEMM_PERSIST
 #define H3K_GEMM_PERSIST 1
@@ -202,12 +224,18 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
   if (!aligned(a, 16) || lda % 16 || !aligned(w8, 16) || ldw % 16)
     return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
   const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
-  const bool big = k % 64 == 0 && m > 512 && n >= 256;
+  // 256 x 256 tiles once at least 5/8 of the CUs get one, smaller tiles of the same pipeline below that.  Measured
+  // (K = 5120 / 13824, N = 5120-15360): 160-240 such tiles beat the smaller ones by 10-20 %, 60-80 lose by 2x.
+  const int tiles256 = ((mm + 255) / 256) * ((nn + 255) / 256);
+  const bool big = k % 64 == 0 && m > 512 && n >= 256 && H3K_MID_FORCE < 0 && tiles256 >= cu_count() * 5 / 8;
   if (H3K_GEMM_PERSIST && big && n % 4 == 0 && k >= gemm_persist_min_k() && aligned(s_ch, 16) && aligned(xs, 16) &&
       (bias == nullptr || aligned(bias, 16)))
     gemm_persist_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
   else if (big)
     gemm_pipe_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
+  else if (k % 64 == 0)
+    gemm_pipe_mid_launch(mid_tile(mm, nn), a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo,
+                         acc_out, st);
   else if (m >= 2048 && n >= 256)
     launch_gemm_dt<4, 4>(a, lda, w8, ldw, mm, nn, kk, xs, s_ch, bias, out, ldo, acc_out, mode, out_dtype, st);
   else if (((m + 127) / 128) * ((n + 127) / 128) >= 256)

@@ -13,6 +13,13 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kBK = 64;
 
+}  // namespace gemm
+
+// Tile shapes of the mid-size pipeline launch (gemm_pipe_mid_launch)
+enum { H3K_MID_64x64 = 0, H3K_MID_64x128 = 1, H3K_MID_128x128 = 2, H3K_MID_128x256 = 3 };
+
+namespace gemm {
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt [11:8])
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -341,7 +341,7 @@ static void launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, i
 }  // namespace persist
 
 // Number of compute units of the current device (cached per device).
-static int cu_count() {
+int cu_count() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

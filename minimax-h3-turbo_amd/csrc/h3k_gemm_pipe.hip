@@ -254,7 +254,55 @@ static void launch_pipe(const int8_t* a, int64_t lda, const int8_t* b, int64_t l
                        dim3(cWM * cWN * 64), 0, st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
 }
 
+// Smaller tiles for shapes with few 256 x 256 tiles (M up to a few thousand rows): the same deep direct-to-LDS
+// pipeline, one stage per barrier.  The register-staged kernel of h3k_gemm.hip keeps a single K-step in flight
+// and is latency-bound there.
+template <int WM, int WN, int WMB, int WNB, int S, int MINB, int ODT, bool EAGER>
+static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
+                       const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
+                       hipStream_t st) {
+  constexpr int BM = 32 * WMB * WM, BN = 32 * WNB * WN;
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  const size_t es = ODT == H3K_F32 ? 4 : 2;
+  const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
+  const bool vec_acc = acc == nullptr || (aligned(acc, 16) && n % 4 == 0);
+  hipLaunchKernelGGL((gemm_pipe_kernel<WM, WN, WMB, WNB, S, 1, MINB, ODT, EAGER>), dim3(tiles), dim3(WM * WN * 64), 0,
+                     st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
+}
+
+template <int ODT, bool EAGER>
+static void launch_mid_cfg(int cfg, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
+                           const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
+                           hipStream_t st) {
+  switch (cfg) {
+    case H3K_MID_128x256:  // 8 waves of 64 x 64, 5 stages of 24 KiB, one workgroup per CU
+      launch_mid<2, 4, 2, 2, 5, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      break;
+    case H3K_MID_128x128:  // 4 waves of 64 x 64, 4 stages of 16 KiB, two workgroups per CU
+      launch_mid<2, 2, 2, 2, 4, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      break;
+    case H3K_MID_64x128:  // 4 waves of 32 x 64, 5 stages of 12 KiB, two workgroups per CU
+      launch_mid<2, 2, 1, 2, 5, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      break;
+    default:  // 64 x 64: 4 waves of 32 x 32, 8 stages of 8 KiB, two workgroups per CU
+      launch_mid<2, 2, 1, 1, 8, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      break;
+  }
+}
+
 }  // namespace pipe
+
+// Mid-size launch: K % 64 == 0, operands as for gemm_pipe_launch; cfg is one of the H3K_MID_* tile shapes.
+void gemm_pipe_mid_launch(int cfg, const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw,
+                          const float* s_ch, const void* bias, int m, int n, int k, int mode, void* out, int odt,
+                          int64_t ldo, int32_t* acc_out, hipStream_t st) {
+  const bool e = mode == H3K_MODE_EAGER;
+#define H3K_L(D, E) pipe::launch_mid_cfg<D, E>(cfg, a, lda, w8, ldw, m, n, k, xs, s_ch, bias, out, ldo, acc_out, st)
+  if (odt == H3K_BF16) { if (e) H3K_L(H3K_BF16, true); else H3K_L(H3K_BF16, false); }
+  else if (odt == H3K_F16) { if (e) H3K_L(H3K_F16, true); else H3K_L(H3K_F16, false); }
+  else { if (e) H3K_L(H3K_F32, true); else H3K_L(H3K_F32, false); }
+#undef H3K_L
+}
 
 // K % 64 == 0, operands 16-byte aligned with 16-byte multiple strides (checked by the caller)
 void gemm_pipe_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8, int64_t ldw, const float* s_ch,

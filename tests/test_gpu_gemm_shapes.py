@@ -1,4 +1,6 @@
-"""The GEMM kernels (persistent and pipelined for large M; 64 x 64 or 128 x 128 tiles for small M) against the CPU oracle
+"""The GEMM kernels (persistent and pipelined on 256 x 256 tiles where at least 160 such tiles exist on 256 CUs;
+the same pipeline on 64 x 64, 64 x 128, 128 x 128 or 128 x 256 tiles below that; the register-staged kernel for K
+not a multiple of 64) against the CPU oracle
 on whole outputs: ragged M and N tails, K-step counts that do not divide the pipeline depth, every epilogue
 variant (ck / eager, bf16 / f16 / f32 out, bias, the int32 accumulator dump, unaligned output strides), and grids
 where every persistent workgroup walks several tiles (full tiles only, and full tiles mixed with cut ones).
@@ -41,8 +43,9 @@ def run(m, n, k, mode, odt, with_bias, ldo_pad=0, acc=False, seed=0):
         assert np.array_equal(accb.cpu().numpy(), want_acc)
 
 
-@pytest.mark.parametrize("m,n,k", [(1100, 520, 640), (700, 256, 64), (513, 1028, 1344), (2304, 768, 192)])
+@pytest.mark.parametrize("m,n,k", [(4100, 2600, 640), (4100, 2602, 192), (2304, 4500, 576), (4200, 2560, 64)])
 def test_large_kernels_ragged_shapes_bf16(m, n, k):
+    # 160-187 tiles of 256 x 256: persistent kernel (K >= 512, N % 4 == 0), per-tile pipeline otherwise
     print(f"gemm m={m} n={n} k={k}", flush=True)
     run(m, n, k, "ck", _lib.BF16, False)
 
@@ -51,12 +54,17 @@ def test_large_kernels_ragged_shapes_bf16(m, n, k):
 @pytest.mark.parametrize("odt", [_lib.BF16, _lib.F16, _lib.F32])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_large_kernels_every_epilogue(mode, odt, with_bias):
-    run(1100, 520, 640, mode, odt, with_bias, seed=3)
+    run(4100, 2600, 640, mode, odt, with_bias, seed=3)  # persistent kernel
+    run(4100, 2602, 192, mode, odt, with_bias, seed=8)  # per-tile pipeline
 
 
-@pytest.mark.parametrize("m,n,k", [(200, 700, 320), (512, 5120, 576), (77, 130, 1040), (512, 8320, 256), (300, 16400, 128)])
+@pytest.mark.parametrize("m,n,k", [(200, 700, 320), (512, 5120, 576), (77, 130, 1040), (512, 8320, 256), (300, 16400, 128),
+                                   (1100, 520, 640), (700, 256, 64), (513, 1028, 1344), (2304, 768, 192),
+                                   (1030, 5000, 512), (600, 3000, 320)])
 def test_small_m_kernel_tile_shapes(m, n, k):
-    # fewer than 256 tiles of 128 x 128: 64 x 64 tiles; otherwise 128 x 128 (ragged M and N in both)
+    # tile shapes picked by tile count on 256 CUs: (200, 700), (1100, 520), (700, 256), (513, 1028) 64 x 64;
+    # (2304, 768), (600, 3000) 64 x 128; (512, 5120), (512, 8320) 128 x 128; (300, 16400), (1030, 5000) 128 x 256;
+    # K=1040 is not a multiple of 64 (register-staged kernel)
     run(m, n, k, "ck", _lib.BF16, False, seed=m + n)
 
 
@@ -64,7 +72,10 @@ def test_small_m_kernel_tile_shapes(m, n, k):
 @pytest.mark.parametrize("odt", [_lib.BF16, _lib.F16, _lib.F32])
 def test_small_m_kernel_every_epilogue(mode, odt):
     run(130, 600, 448, mode, odt, True, ldo_pad=8, acc=True, seed=3)  # 64 x 64 tiles
+    run(260, 4000, 256, mode, odt, True, ldo_pad=8, acc=True, seed=5)  # 64 x 128 tiles
     run(384, 11000, 192, mode, odt, True, ldo_pad=8, acc=True, seed=4)  # 128 x 128 tiles
+    run(500, 13000, 320, mode, odt, True, ldo_pad=8, acc=True, seed=6)  # 128 x 256 tiles
+    run(130, 600, 464, mode, odt, True, ldo_pad=8, acc=True, seed=7)  # K % 64 != 0: register-staged kernel
 
 
 @pytest.mark.parametrize("m,n,k", [(6144, 8448, 512), (5000, 8000, 576)])
@@ -74,5 +85,6 @@ def test_persistent_kernel_walks_several_tiles_per_workgroup(m, n, k):
 
 
 def test_large_kernels_accumulator_dump_and_unaligned_output_rows():
-    run(1100, 520, 640, "ck", _lib.BF16, True, ldo_pad=1, acc=True, seed=4)
-    run(1030, 772, 256, "eager", _lib.F32, False, ldo_pad=3, acc=True, seed=5)
+    run(4100, 2600, 640, "ck", _lib.BF16, True, ldo_pad=1, acc=True, seed=4)
+    run(4100, 2604, 256, "eager", _lib.F32, False, ldo_pad=3, acc=True, seed=5)
+    run(1030, 772, 256, "eager", _lib.F32, False, ldo_pad=3, acc=True, seed=5)  # 64 x 64 tiles
