@@ -224,10 +224,15 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
   if (!aligned(a, 16) || lda % 16 || !aligned(w8, 16) || ldw % 16)
     return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
   const int mm = static_cast<int>(m), nn = static_cast<int>(n), kk = static_cast<int>(k);
-  // 256 x 256 tiles once at least 5/8 of the CUs get one, smaller tiles of the same pipeline below that.  Measured
-  // (K = 5120 / 13824, N = 5120-15360): 160-240 such tiles beat the smaller ones by 10-20 %, 60-80 lose by 2x.
-  const int tiles256 = ((mm + 255) / 256) * ((nn + 255) / 256);
-  const bool big = k % 64 == 0 && m > 512 && n >= 256 && H3K_MID_FORCE < 0 && tiles256 >= cu_count() * 5 / 8;
+  // 256 x 256 tiles once at least 5/8 of the CUs get one and their last round of tiles is not mostly idle; smaller
+  // tiles of the same pipeline otherwise.  Measured (K = 5120 / 13824, N = 5120-15360): 160-240 such tiles beat
+  // the smaller ones by 10-20 %, 60-80 lose by 2x; at full occupancy 128 x 256 tiles run at 0.83 of the 256 x 256
+  // rate, so M=4096 N=5120 (320 tiles: 1.25 rounds) goes faster on 640 tiles of 128 x 256 (+5-14 %).
+  const int cus = cu_count();
+  const int tiles256 = ((mm + 255) / 256) * ((nn + 255) / 256), tiles128x256 = ((mm + 127) / 128) * ((nn + 255) / 256);
+  auto fill = [cus](int t) { return static_cast<double>(t) / (static_cast<double>((t + cus - 1) / cus) * cus); };
+  const bool big = k % 64 == 0 && m > 512 && n >= 256 && H3K_MID_FORCE < 0 && tiles256 >= cus * 5 / 8 &&
+                   fill(tiles256) >= 0.83 * fill(tiles128x256);
   if (H3K_GEMM_PERSIST && big && n % 4 == 0 && k >= gemm_persist_min_k() && aligned(s_ch, 16) && aligned(xs, 16) &&
       (bias == nullptr || aligned(bias, 16)))
     gemm_persist_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
