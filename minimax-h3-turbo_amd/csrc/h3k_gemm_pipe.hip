@@ -270,16 +270,25 @@ static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ld
                      st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
 }
 
+// Ring depths of the two larger mid-size tiles.  4-6 stages (128 x 256) and 3-5 (128 x 128) measured within run-to-run
+// noise of each other at M = 128-1024, K = 5120 / 13824, N = 5120-15360.
+#ifndef H3K_MID_S_128x256
+#define H3K_MID_S_128x256 5
+#endif
+#ifndef H3K_MID_S_128x128
+#define H3K_MID_S_128x128 4
+#endif
+
 template <int ODT, bool EAGER>
 static void launch_mid_cfg(int cfg, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
                            const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
                            hipStream_t st) {
   switch (cfg) {
     case H3K_MID_128x256:  // 8 waves of 64 x 64, 5 stages of 24 KiB, one workgroup per CU
-      launch_mid<2, 4, 2, 2, 5, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      launch_mid<2, 4, 2, 2, H3K_MID_S_128x256, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
     case H3K_MID_128x128:  // 4 waves of 64 x 64, 4 stages of 16 KiB, two workgroups per CU
-      launch_mid<2, 2, 2, 2, 4, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      launch_mid<2, 2, 2, 2, H3K_MID_S_128x128, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
     case H3K_MID_64x128:  // 4 waves of 32 x 64, 5 stages of 12 KiB, two workgroups per CU
       launch_mid<2, 2, 1, 2, 5, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
