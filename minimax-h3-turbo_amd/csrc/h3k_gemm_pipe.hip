@@ -257,7 +257,8 @@ static void launch_pipe(const int8_t* a, int64_t lda, const int8_t* b, int64_t l
 // Smaller tiles for shapes with few 256 x 256 tiles (M up to a few thousand rows): the same deep direct-to-LDS
 // pipeline, one stage per barrier.  The register-staged kernel of h3k_gemm.hip keeps a single K-step in flight
 // and is latency-bound there.
-template <int WM, int WN, int WMB, int WNB, int S, int MINB, int ODT, bool EAGER>
+// U K-steps per barrier where the K-step count allows it (one otherwise).
+template <int WM, int WN, int WMB, int WNB, int S, int U, int MINB, int ODT, bool EAGER>
 static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
                        const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
                        hipStream_t st) {
@@ -266,12 +267,17 @@ static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ld
   const size_t es = ODT == H3K_F32 ? 4 : 2;
   const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
   const bool vec_acc = acc == nullptr || (aligned(acc, 16) && n % 4 == 0);
-  hipLaunchKernelGGL((gemm_pipe_kernel<WM, WN, WMB, WNB, S, 1, MINB, ODT, EAGER>), dim3(tiles), dim3(WM * WN * 64), 0,
-                     st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
+  if (U > 1 && (k / kBK) % U == 0)
+    hipLaunchKernelGGL((gemm_pipe_kernel<WM, WN, WMB, WNB, S, U, MINB, ODT, EAGER>), dim3(tiles), dim3(WM * WN * 64), 0,
+                       st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
+  else
+    hipLaunchKernelGGL((gemm_pipe_kernel<WM, WN, WMB, WNB, S, 1, MINB, ODT, EAGER>), dim3(tiles), dim3(WM * WN * 64), 0,
+                       st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
 }
 
 // Ring depths of the two larger mid-size tiles.  4-6 stages (128 x 256) and 3-5 (128 x 128) measured within run-to-run
-// noise of each other at M = 128-1024, K = 5120 / 13824, N = 5120-15360.
+// noise of each other at M = 128-1024, K = 5120 / 13824, N = 5120-15360.  Two K-steps per barrier make the 64-row
+// tiles faster (64 x 64 +12-14 %, 64 x 128 +2-7 %) and the 128-row ones slower (-7 to -11 %).
 #ifndef H3K_MID_S_128x256
 #define H3K_MID_S_128x256 5
 #endif
@@ -279,22 +285,23 @@ static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ld
 #define H3K_MID_S_128x128 4
 #endif
 
+
 template <int ODT, bool EAGER>
 static void launch_mid_cfg(int cfg, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
                            const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
                            hipStream_t st) {
   switch (cfg) {
     case H3K_MID_128x256:  // 8 waves of 64 x 64, 5 stages of 24 KiB, one workgroup per CU
-      launch_mid<2, 4, 2, 2, H3K_MID_S_128x256, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      launch_mid<2, 4, 2, 2, H3K_MID_S_128x256, 1, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
     case H3K_MID_128x128:  // 4 waves of 64 x 64, 4 stages of 16 KiB, two workgroups per CU
-      launch_mid<2, 2, 2, 2, H3K_MID_S_128x128, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      launch_mid<2, 2, 2, 2, H3K_MID_S_128x128, 1, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
-    case H3K_MID_64x128:  // 4 waves of 32 x 64, 5 stages of 12 KiB, two workgroups per CU
-      launch_mid<2, 2, 1, 2, 5, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+    case H3K_MID_64x128:  // 4 waves of 32 x 64, 5 stages of 12 KiB, two workgroups per CU, 2 K-steps per barrier
+      launch_mid<2, 2, 1, 2, 5, 2, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
-    default:  // 64 x 64: 4 waves of 32 x 32, 8 stages of 8 KiB, two workgroups per CU
-      launch_mid<2, 2, 1, 1, 8, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+    default:  // 64 x 64: 4 waves of 32 x 32, 8 stages of 8 KiB, two workgroups per CU, 2 K-steps per barrier
+      launch_mid<2, 2, 1, 1, 8, 2, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
   }
 }
