@@ -51,9 +51,10 @@ static size_t weight_region(int64_t m, int64_t n, int64_t k) {
   return grid > acc ? grid : acc;
 }
 
-// Chunks of up to 64 rows take the fused int4 GEMM; from ~100 rows the decode + int8 GEMM pair is faster.
+// Chunks of up to 32 rows take the fused int4 GEMM; from 64 rows the decode + int8 GEMM pair is faster (N=13824,
+// K=5120: 35 against 42 us at 64 rows), at 16 the fused GEMM (15 against 34 us).
 static bool fused_few_rows(int64_t m, int64_t k, int group, const void* q, int64_t ldq) {
-  return m <= 64 && k % 64 == 0 && (group == 16 || group == 32 || (group > 0 && group % 64 == 0)) && k % group == 0 &&
+  return m <= 32 && k % 64 == 0 && (group == 16 || group == 32 || (group > 0 && group % 64 == 0)) && k % group == 0 &&
          aligned(q, 16) && ldq % 16 == 0;
 }
 

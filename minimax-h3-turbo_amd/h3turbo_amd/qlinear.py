@@ -250,9 +250,10 @@ def _swiglu(x: torch.Tensor) -> torch.Tensor:
     return F.silu(gate).mul_(up)
 
 
-# token chunks up to this many rows take the fused int4 GEMM (h3k_gemm_w4a8); at 128 rows the per-call decode + int8
-# GEMM pair is faster (N=13824, K=5120: 54 against 74 us), at 64 the fused GEMM (42 against 54 us)
-FEW_ROWS = 64
+# token chunks up to this many rows take the fused int4 GEMM (h3k_gemm_w4a8); above it the per-call decode + int8
+# GEMM pair is faster (N=13824, K=5120, g128 fp16: 35 against 42 us at 64 rows, 44 against 73 at 128), at 16 the
+# fused GEMM (15 against 34 us)
+FEW_ROWS = 32
 
 
 class _HipRunner:
