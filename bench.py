@@ -90,11 +90,22 @@ def synth_weight(n: int, k: int, dev, seed: int = 0, group: int = 128, convrot: 
     return q, s_rel, s_ch, cb
 
 
-def gemm_kernel_name(m: int, n: int, k: int) -> str:
-    """The GEMM kernel h3k_gemm_a8w8 dispatches for this shape with aligned operands (the rule of
-    gemm_a8w8_launch in h3k_gemm.hip)."""
-    if k % 64 == 0 and m > 512 and n >= 256:
-        return "gemm_persist_kernel" if n % 4 == 0 and k >= 512 else "gemm_pipe_kernel"
+def gemm_kernel_name(m: int, n: int, k: int, packed: bool, cus: int = 256) -> str:
+    """The GEMM kernel the W4A8 linear runs for this shape with aligned operands: the packed-weight kernel where
+    h3k_gemm_packed_serves accepts the shape, otherwise the rule of gemm_a8w8_launch (h3k_gemm.hip)."""
+    if packed:
+        return "gemm_w8p_kernel"
+    t256 = -(-m // 256) * -(-n // 256)
+    t128 = -(-m // 128) * -(-n // 256)
+
+    def fill(t):
+        return t / (-(-t // cus) * cus)
+
+    big = k % 64 == 0 and m > 512 and n >= 256 and t256 >= cus * 5 // 8 and fill(t256) >= 0.83 * fill(t128)
+    if big and n % 4 == 0 and k >= 512:
+        return "gemm_persist_kernel"
+    if k % 64 == 0:
+        return "gemm_pipe_kernel"
     return "gemm_a8w8_kernel"
 
 
@@ -586,9 +597,10 @@ def main() -> None:
 
     lib = _lib.load()
     dw = ql._DevWeight(w)
+    packed = bool(lib.h3k_gemm_packed_serves(m, n, k))
     xq = torch.empty(m, k, dtype=torch.int8, device=dev)
     xs = torch.empty(m, 1, dtype=torch.float32, device=dev)
-    w8 = torch.empty(n, k, dtype=torch.int8, device=dev)
+    w8 = torch.empty(lib.h3k_w8_packed_bytes(n, k) if packed else n * k, dtype=torch.int8, device=dev)
     out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
@@ -605,11 +617,19 @@ def main() -> None:
         e0 = mark()
         _lib.check(lib.h3k_rotate_quant(x.data_ptr(), _lib.BF16, m, k, k, 256, 0, xq.data_ptr(), k, xs.data_ptr(), sp), "rq")
         e1 = mark()
-        _lib.check(lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(), n, k, 128,
-                                     w8.data_ptr(), k, sp), "decode")
+        if packed:  # the route qlinear.linear takes for this shape: packed weight grid + packed-weight GEMM
+            _lib.check(lib.h3k_decode_w4_packed(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds,
+                                                dw.cb.data_ptr(), n, k, 128, w8.data_ptr(), sp), "decode")
+        else:
+            _lib.check(lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(), n,
+                                         k, 128, w8.data_ptr(), k, sp), "decode")
         e2 = mark()
-        _lib.check(lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, dw.s_ch.data_ptr(), None, m, n, k, 0,
-                                     out.data_ptr(), _lib.BF16, n, None, sp), "gemm")
+        if packed:
+            _lib.check(lib.h3k_gemm_a8w8_packed(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), dw.s_ch.data_ptr(), None,
+                                                m, n, k, 0, out.data_ptr(), _lib.BF16, n, None, sp), "gemm")
+        else:
+            _lib.check(lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, dw.s_ch.data_ptr(), None, m,
+                                         n, k, 0, out.data_ptr(), _lib.BF16, n, None, sp), "gemm")
         e3 = mark()
         if record:
             ev["rq"].append((e0, e1))
@@ -637,6 +657,7 @@ def main() -> None:
 
     t_rq, t_dec, t_gemm = mean_ms(ev["rq"]), mean_ms(ev["dec"]), mean_ms(ev["gemm"])
     ops = 2.0 * m * n * k
+    kname = gemm_kernel_name(m, n, k, packed, torch.cuda.get_device_properties(dev).multi_processor_count)
     tops = ops / (ms_step * 1e-3) / 1e12
     gemm_tops = ops / (t_gemm * 1e-3) / 1e12
     rq_bytes = 2 * m * k + m * k + 4 * m
@@ -659,8 +680,8 @@ def main() -> None:
                    "m": m, "k": k, "n": n, "group": 128, "convrot": 256},
         "pct_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(f"{gemm_kernel_name(m, n, k)} m={m} k={k} n={n}"),
-                     "kernel": gemm_kernel_name(m, n, k), "kernel_ms": round(t_gemm, 4)},
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(f"{kname} m={m} k={k} n={n}"),
+                     "kernel": kname, "kernel_ms": round(t_gemm, 4)},
         "kernels": {
             "rotate_quant": {"ms": round(t_rq, 4), "GB/s": round(rq_bytes / (t_rq * 1e-3) / 1e9, 1),
                              "frac_hbm": round(rq_bytes / (t_rq * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},

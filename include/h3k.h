@@ -37,7 +37,7 @@ extern "C" {
 #define H3K_ELAUNCH -2  /* a HIP runtime call or kernel launch failed */
 #define H3K_ESPACE -3   /* workspace too small */
 
-/* ABI version (bumped on any signature change). */
+/* ABI version (bumped on any signature change or addition). */
 int h3k_version(void);
 
 /* Message of the last failure on this thread ("" if none). */
@@ -85,6 +85,42 @@ int h3k_gemm_a8w8(const int8_t* a, int64_t lda, const float* xs, const int8_t* w
                   int32_t* acc_out, void* stream);
 
 /*
+ * The packed int8 weight grid of the large-shape GEMM: K-steps t of 64 bytes by blocks b of 32 weight rows (n padded
+ * with zero rows to a multiple of 256; NBP = padded n / 32), block (t, b) at byte (t * NBP + b) * 2048 as two 1 KiB
+ * MFMA operand fragments in which lane l holds row 32b + (l & 31), bytes 64t + 32(l >> 5) + 16h .. + 16 (h = 0, 1).
+ * Same levels as the row-major grid of h3k_decode_w4, another order.  k must be a multiple of 64.
+ */
+int64_t h3k_w8_packed_bytes(int64_t n, int64_t k); /* size of the packed grid, -1 for a bad shape */
+
+/*
+ * int4 codebook indices -> the packed int8 grid (same levels as h3k_decode_w4).
+ * Replaces h3turbo/h3/qlinear.py:194-204 (decode_int8_grid) where the grid feeds the large-shape GEMM.
+ *   q packed [n, k/2] (ldq bytes, 16-byte aligned, ldq a multiple of 16); s_rel, codebook as for h3k_decode_w4;
+ *   w8p h3k_w8_packed_bytes(n, k) bytes, 16-byte aligned
+ */
+int h3k_decode_w4_packed(const void* q, int64_t ldq, const void* s_rel, int s_dtype, int64_t lds, const float* codebook,
+                         int64_t n, int64_t k, int group, int8_t* w8p, void* stream);
+
+/* Row-major int8 grid [n, k] (ldw bytes, 16-byte aligned) -> the packed grid.  A layout change, no reference
+ * counterpart: for callers holding a decoded grid. */
+int h3k_pack_w8(const int8_t* w8, int64_t ldw, int64_t n, int64_t k, int8_t* w8p, void* stream);
+
+/* 1 when h3k_gemm_a8w8_packed serves an m x n x k GEMM (k a multiple of 256, at least 512; enough 256 x 256 output
+ * tiles to fill the chip), else 0. */
+int h3k_gemm_packed_serves(int64_t m, int64_t n, int64_t k);
+
+/*
+ * h3k_gemm_a8w8 over the packed weight grid, for the shapes h3k_gemm_packed_serves accepts: the weight fragments
+ * go from L2 straight into registers, only the activations are staged through LDS.  Same contract and bit-identical
+ * results as h3k_gemm_a8w8.
+ * Replaces h3turbo/h3/qlinear.py:236-254 (_int8_mm) and :396-405 (_TorchRunner._a8 epilogue).
+ *   a [m, k] int8 (lda bytes, 16-byte aligned, (m-1)*lda + k < 2^32), xs/s_ch/bias 16-byte aligned
+ */
+int h3k_gemm_a8w8_packed(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
+                         const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out, int out_dtype,
+                         int64_t ldo, int32_t* acc_out, void* stream);
+
+/*
  * W4A8 GEMM for few token rows (m <= 128): the int4 weight is decoded in registers into the int8 MFMA operands,
  * so the int8 grid is never written; exact int32 accumulators and the epilogue of h3k_gemm_a8w8.
  * Replaces, fused, h3turbo/h3/qlinear.py:157-204 (decode_int8_grid), :236-254 (_int8_mm) and :396-405 (_a8
@@ -103,8 +139,9 @@ int h3k_gemm_w4a8(const int8_t* a, int64_t lda, const float* xs, const void* q, 
                   int32_t* acc_out, void* stream);
 
 /*
- * The whole W4A8 ConvRot linear: rotate+quantise x, decode the weight, GEMM + epilogue (m <= 64 with k a multiple
- * of 64: the fused few-row GEMM, no decode pass).
+ * The whole W4A8 ConvRot linear: rotate+quantise x, decode the weight, GEMM + epilogue.  m <= 32 with k a multiple
+ * of 64: the fused few-row GEMM, no decode pass; shapes h3k_gemm_packed_serves accepts: the packed grid and its
+ * GEMM; otherwise the row-major grid and h3k_gemm_a8w8.
  * Fills the slot of comfy_kitchen's w4a8_int8_linear call, h3turbo/h3/qlinear.py:427-429 (_run_ck).
  * workspace: device scratch of at least h3k_w4a8_linear_workspace(m, n, k) bytes, 256-byte aligned.
  */

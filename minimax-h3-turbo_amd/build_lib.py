@@ -48,6 +48,20 @@ def _run(cmd, verbose):
         print(out, flush=True)
 
 
+def guard_weight_loads(obj: str) -> None:
+    """Fail the build when the compiler touched an in-flight inline-assembly weight register (asm_guard.py)."""
+    sys.path.insert(0, HERE)
+    import asm_guard
+
+    if not asm_guard.available():
+        raise RuntimeError("llvm-objcopy / clang-offload-bundler / llvm-objdump not found under /opt/rocm/llvm/bin: "
+                           "the weight-register guard of h3k_gemm_w8p.o cannot run")
+    bad = asm_guard.check_object(obj)
+    if bad:
+        raise RuntimeError("h3k_gemm_w8p.o: the compiler touches asynchronous weight registers in flight:\n  " +
+                           "\n  ".join(bad[:10]))
+
+
 def build(jobs: int = 4, verbose: bool = False) -> str:
     cc = hipcc()
     os.makedirs(BUILD, exist_ok=True)
@@ -57,6 +71,7 @@ def build(jobs: int = 4, verbose: bool = False) -> str:
         futs = [ex.submit(_run, [cc, *FLAGS, "-c", os.path.join(CSRC, s), "-o", o], verbose) for s, o in zip(srcs, objs)]
         for f in futs:
             f.result()
+    guard_weight_loads(os.path.join(BUILD, "h3k_gemm_w8p.o"))
     tmp = OUT + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, OUT)

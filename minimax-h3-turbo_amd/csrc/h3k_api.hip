@@ -36,19 +36,33 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
 
 static inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+int64_t w8p_bytes(int64_t n, int64_t k);
+bool w8p_serves(int64_t m, int64_t n, int64_t k);
+void gemm_w8p_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
+                     const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo, int32_t* acc_out,
+                     hipStream_t st);
+
 }  // namespace h3k
 
 using namespace h3k;
 
-extern "C" int h3k_version(void) { return 1; }
+extern "C" int h3k_version(void) { return 2; }
 
 extern "C" const char* h3k_last_error(void) { return g_last_error.c_str(); }
 
-// The weight region holds the decoded int8 grid, or for the fused few-row GEMM its split-K accumulators.
+// The weight region holds the decoded int8 grid (row-major, or packed: n rounded up to 256 rows), or for the fused
+// few-row GEMM its split-K accumulators.
 static size_t weight_region(int64_t m, int64_t n, int64_t k) {
-  const size_t grid = static_cast<size_t>(n) * k;
+  const size_t grid = static_cast<size_t>((n + 255) / 256 * 256) * k;
   const size_t acc = static_cast<size_t>(h3k_gemm_w4a8_workspace(m, n, k));
   return grid > acc ? grid : acc;
+}
+
+// The packed grid and its GEMM: shapes with enough 256 x 256 tiles, the rotate+quant output (lda = k) addressable
+// by one buffer descriptor, and a packed weight the packed decode can read.
+static bool packed_route(int64_t m, int64_t n, int64_t k, const void* q, int64_t ldq, int group) {
+  return w8p_serves(m, n, k) && (m - 1) * k + k < (int64_t(1) << 32) && aligned(q, 16) && ldq % 16 == 0 &&
+         group >= 4 && k % group == 0 && ((16 % group) == 0 || (group % 16) == 0);
 }
 
 // Chunks of up to 32 rows take the fused int4 GEMM; from 64 rows the decode + int8 GEMM pair is faster (N=13824,
@@ -83,6 +97,15 @@ extern "C" int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k,
   if (fused_few_rows(m, k, group, q, ldq))  // int4 decoded in registers: no int8 grid
     return h3k_gemm_w4a8(aq, k, xs, q, ldq, s_rel, s_dtype, lds, codebook, group, s_ch, bias, m, n, k, mode, out,
                          out_dtype, ldo, reinterpret_cast<int32_t*>(w8), nullptr, stream);
+  if (packed_route(m, n, k, q, ldq, group) && aligned(s_ch, 16) && (bias == nullptr || aligned(bias, 16)) &&
+      ldo >= n && (mode == H3K_MODE_CK || mode == H3K_MODE_EAGER) &&
+      (out_dtype == H3K_BF16 || out_dtype == H3K_F16 || out_dtype == H3K_F32) && out) {
+    rc = h3k_decode_w4_packed(q, ldq, s_rel, s_dtype, lds, codebook, n, k, group, w8, stream);
+    if (rc) return rc;
+    gemm_w8p_launch(aq, k, xs, w8, s_ch, bias, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), mode, out,
+                    out_dtype, ldo, nullptr, static_cast<hipStream_t>(stream));
+    return check_launch("gemm_a8w8_packed");
+  }
   rc = h3k_decode_w4(q, ldq, s_rel, s_dtype, lds, codebook, n, k, group, w8, k, stream);
   if (rc) return rc;
   return gemm_a8w8_launch(aq, k, xs, w8, k, s_ch, bias, m, n, k, mode, out, out_dtype, ldo, nullptr,

@@ -98,6 +98,81 @@ __global__ __launch_bounds__(256) void decode_w4_lut_kernel(const uint8_t* __res
   *reinterpret_cast<u32x4*>(dst + 16) = u32x4{o[4], o[5], o[6], o[7]};
 }
 
+// The same levels written in the packed layout of the large-shape GEMM (h3k_gemm_w8p.hip): 64-byte K-steps t of
+// 32-row blocks b (N padded to a multiple of 256 rows), block (t, b) 2 KiB at (t * NBP + b) * 2048 as two 1 KiB MFMA
+// fragments in which lane l holds row 32b + (l & 31), bytes 64t + 32(l >> 5) + 16h .. + 16.  A thread owns one row's
+// 32 consecutive levels (16 packed bytes in, the two 16-byte halves out), and threads are numbered in packed order,
+// so a wavefront's two stores are each 1 KiB contiguous.  Rows past n (the padding) are written as zeros.  GK: 0 for groups that are multiples of 32
+// (one scale per thread, its 16 levels as a byte table), 1 for group 16 (two tables), 2 for groups 4 and 8 (levels
+// computed per element).
+template <int SD, int GK>
+__global__ __launch_bounds__(256) void decode_w4_packed_kernel(const uint8_t* __restrict__ q, int64_t ldq,
+                                                               const void* __restrict__ s_rel, int64_t lds,
+                                                               const float* __restrict__ cb, int n, int nbp,
+                                                               int group, int8_t* __restrict__ wp, int64_t threads) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (u >= threads) return;
+  const int l = static_cast<int>(u & 63);
+  const int64_t bt = u >> 6;  // t * NBP + b
+  const int b = static_cast<int>(bt % nbp);
+  const int t = static_cast<int>(bt / nbp);
+  const int row = b * 32 + (l & 31);
+  const int k0 = t * 64 + (l >> 5) * 32;  // first of this thread's 32 levels
+  int8_t* dst = wp + bt * 2048 + l * 16;
+  if (row >= n) {
+    *reinterpret_cast<u32x4*>(dst) = u32x4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4*>(dst + 1024) = u32x4{0u, 0u, 0u, 0u};
+    return;
+  }
+  const u32x4 pk = *reinterpret_cast<const u32x4*>(q + static_cast<int64_t>(row) * ldq + k0 / 2);
+  const int64_t srow = static_cast<int64_t>(row) * lds;
+  uint32_t o[8];
+  if constexpr (GK == 2) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = w * 4 + e;  // level index within the 32
+        const uint32_t byte = (pk[i >> 3] >> (8 * ((i >> 1) & 3))) & 0xFFu;
+        const uint32_t nib = (i & 1) ? (byte >> 4) : (byte & 0xFu);
+        v |= level(cb[nib], load_scale<SD>(s_rel, srow + (k0 + i) / group)) << (8 * e);
+      }
+      o[w] = v;
+    }
+  } else {
+    float cbv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cbv[i] = cb[i];
+    const bool cb_finite = all_finite(cbv);
+    uint32_t lut[4];
+    build_lut_fast(cbv, cb_finite, load_scale<SD>(s_rel, srow + k0 / group), lut);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {  // 4 packed bytes -> 8 levels
+      if (GK == 1 && w == 2) build_lut_fast(cbv, cb_finite, load_scale<SD>(s_rel, srow + (k0 + 16) / group), lut);
+      lut_decode_word(lut, pk[w], o[2 * w], o[2 * w + 1]);
+    }
+  }
+  *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+  *reinterpret_cast<u32x4*>(dst + 1024) = u32x4{o[4], o[5], o[6], o[7]};
+}
+
+template <int SD>
+static void launch_decode_packed(const void* q, int64_t ldq, const void* s_rel, int64_t lds, const float* cb, int64_t n,
+                                 int k, int group, int8_t* wp, hipStream_t st) {
+  const int nbp = static_cast<int>((n + 255) / 256 * 8);
+  const int64_t threads = static_cast<int64_t>(nbp) * 32 * (k / 32);
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  const uint8_t* qb = static_cast<const uint8_t*>(q);
+  const int nn = static_cast<int>(n);
+  if (group % 32 == 0)
+    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 0>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, threads);
+  else if (group == 16)
+    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 1>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, threads);
+  else
+    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 2>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, threads);
+}
+
 template <int SD>
 static void launch_decode(const void* q, int64_t ldq, const void* s_rel, int64_t lds, const float* cb, int64_t n, int k,
                           int group, int8_t* w8, int64_t ldw, hipStream_t st) {
@@ -150,4 +225,31 @@ extern "C" int h3k_decode_w4(const void* q, int64_t ldq, const void* s_rel, int 
     default: launch_decode<H3K_F32>(q, ldq, s_rel, lds, codebook, n, kk, group, w8, ldw, st); break;
   }
   return check_launch("decode_w4");
+}
+
+extern "C" int h3k_decode_w4_packed(const void* q, int64_t ldq, const void* s_rel, int s_dtype, int64_t lds,
+                                    const float* codebook, int64_t n, int64_t k, int group, int8_t* w8p,
+                                    void* stream) {
+  if (s_dtype != H3K_FP8E4M3 && s_dtype != H3K_F16 && s_dtype != H3K_BF16 && s_dtype != H3K_F32)
+    return fail(H3K_EINVAL, "s_rel dtype code %d unsupported (fp8e4m3/f16/bf16/f32)", s_dtype);
+  if (group < 4 || k <= 0 || k % 64 || k % group || ((16 % group) && (group % 16)))
+    return fail(H3K_EINVAL,
+                "K=%lld must be divisible by 64 and group_size=%d; group_size >= 4 dividing 16 or a multiple of 16",
+                (long long)k, group);
+  if (n < 0 || n > (1 << 30) || k > (1 << 30) || (n + 255) / 256 * 256 * k >= (int64_t(1) << 40))
+    return fail(H3K_EINVAL, "bad n/k");
+  if (ldq < k / 2 || lds < k / group) return fail(H3K_EINVAL, "row strides smaller than the rows");
+  if (n == 0) return H3K_OK;
+  if (!q || !s_rel || !codebook || !w8p) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(q, 16) || ldq % 16 || !aligned(w8p, 16))
+    return fail(H3K_EINVAL, "q must be 16-byte aligned with a 16-byte multiple row stride, w8p 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int kk = static_cast<int>(k);
+  switch (s_dtype) {
+    case H3K_FP8E4M3: launch_decode_packed<H3K_FP8E4M3>(q, ldq, s_rel, lds, codebook, n, kk, group, w8p, st); break;
+    case H3K_F16: launch_decode_packed<H3K_F16>(q, ldq, s_rel, lds, codebook, n, kk, group, w8p, st); break;
+    case H3K_BF16: launch_decode_packed<H3K_BF16>(q, ldq, s_rel, lds, codebook, n, kk, group, w8p, st); break;
+    default: launch_decode_packed<H3K_F32>(q, ldq, s_rel, lds, codebook, n, kk, group, w8p, st); break;
+  }
+  return check_launch("decode_w4_packed");
 }

@@ -1,0 +1,494 @@
+// Large-shape int8 GEMM over a fragment-ordered ("packed") int8 weight grid, W4A8 epilogue fused:
+//   acc[m, n] = sum_k a[m, k] * w8[n, k]                         exact int32
+//   ck   : out = round(f32(f32(acc) * xs[m]) * s_ch[n])          reference h3turbo/h3/qlinear.py:401
+//   eager: out = round(f32(acc) * f32(xs[m] * s_ch[n]))          reference h3turbo/h3/qlinear.py:403
+//   bias : out = round(f32(out) + f32(bias[n]))                  reference h3turbo/h3/qlinear.py:404-405
+//
+// Packed weight layout.  The grid is cut into K-steps of 64 bytes and blocks of 32 weight rows, N padded with zero
+// rows to a multiple of 256 (a whole output tile).  Step t, block b is 2 KiB at ((t * NBP + b) * 2 + h) * 1024 +
+// lane * 16 (NBP = padded N / 32): the 16-byte MFMA fragment of lane `lane` for half h, i.e. row 32b + (lane & 31),
+// bytes 64t + 32(lane >> 5) + 16h .. + 16.  Lanes 0-31 own the first 32 bytes of the step, lanes 32-63 the last
+// 32; any permutation of k applied to both operands leaves the dot products unchanged, and the activation fragments
+// are read from LDS in the same order.  One 16-byte load per lane fetches a whole 1 KiB fragment, and the 4 blocks a
+// wavefront multiplies at one step are 8 KiB in one piece.
+//
+// Why: the row-major kernels stage both operands through LDS, and at full MFMA rate their 96 KiB of fragment reads
+// plus 32 KiB of direct-to-LDS writes per K-step (256 x 256 tile) run the LDS at 60-75 % of its measured read
+// rate, a co-limiter next to the power ceiling.  Here only the activations go through LDS: a workgroup of 4
+// wavefronts (2 x 2, one per SIMD) owns a 256 x 256 tile, each wavefront 128 x 128 outputs as 4 x 4 blocks of
+// v_mfma_i32_32x32x32_i8, so per K-step the LDS sees 16 KiB of DMA writes and 32 KiB of fragment reads (48 KiB
+// instead of 128).  The weight fragments go straight from L2 into registers through buffer loads, S K-steps
+// ahead, in a register ring of S x 32 VGPRs.
+//
+// Schedule (the persistent form of h3k_gemm_persist.hip): one workgroup per CU walks tiles t = blockIdx +
+// i * gridDim in the XCD-aware order of tile_coords; the activation DMA stream and the weight register stream both
+// run across tile boundaries (the last S steps of a tile issue the next tile's first S steps).  Per step, after
+// the barrier: the DMA of stage kt + S into the stage just read; after the second half's MFMAs: the weight
+// fragments of step kt + S into the registers just consumed.  vmcnt retires in issue order, so the wait before a
+// step's barrier allows exactly the ops of the S - 2 newer steps (G each) -- plus, in the S - 1 steps after a
+// full-tile epilogue, its NEPI stores.  The epilogue stages each 32-row block of a wavefront's outputs through a
+// private LDS area and stores whole 128-byte lines, non-temporally.
+#include "h3k_gemm_common.hpp"
+
+namespace h3k {
+namespace w8p {
+
+using namespace gemm;
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+constexpr int kBlockBytes = 2048;  // one 32-row block, one 64-byte K-step
+
+// Buffer descriptor of the packed weights as four scalar words (base, stride 0, num_records, raw-buffer flags).
+__device__ __forceinline__ u32x4 weight_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+
+// One 16-byte weight fragment load into registers, as inline assembly.  The compiler's wait insertion treats the
+// direct-to-LDS loads and register-returning buffer loads as counters that may retire out of order, and where both
+// are pending it can only wait for vmcnt(0): with builtin loads it drained vmcnt at the top of every group of S
+// steps.  The assembly load is invisible to it, and the kernel's explicit waits cover it: the fragments of step kt
+// are part of the group whose arrival the wait before step kt - 1's barrier enforces.  Nothing but an MFMA reads
+// the destination registers, and none before that wait.
+template <int OFF>
+__device__ __forceinline__ void weight_load(v4i& dst, const u32x4& rsrc, uint32_t voff, uint32_t soff) {
+  __asm__ volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:%4"
+                   : "=&v"(dst)
+                   : "v"(voff), "s"(rsrc), "s"(soff), "n"(OFF));
+}
+
+template <int S, int ODT, bool EAGER, bool ACC>
+__global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restrict__ A, int64_t lda,
+                                                          const int8_t* __restrict__ Bp, uint32_t bp_bytes, int NBP,
+                                                          int M, int N, int K, const float* __restrict__ xs,
+                                                          const float* __restrict__ sch, const void* __restrict__ bias,
+                                                          void* __restrict__ out, int64_t ldo,
+                                                          int32_t* __restrict__ acc_out, bool vec_out) {
+  constexpr int WMB = 4, WNB = 4;   // a wavefront's 4 x 4 blocks of 32 x 32
+  constexpr int BM = 256, BN = 256;
+  constexpr int STAGE = BM * kBK;   // 16 KiB of activations per K-step
+  constexpr int DPW = STAGE / 1024 / 4;  // 1 KiB direct-to-LDS loads per wavefront per stage
+  constexpr int BPW = 2 * WNB;           // weight fragment loads per wavefront per step
+  constexpr int G = DPW + BPW;           // vector-memory ops per wavefront per step
+  constexpr bool STAGED = ODT != H3K_F32;
+  constexpr int NEPI = 8 * WMB;          // stores of one full-tile 16-bit epilogue per wavefront
+  constexpr int GROW = 132;              // staging row pitch: 128 32-bit values + 4 of padding
+  constexpr int RS = 2;                  // scale slots (tile t uses slot t % 2)
+  constexpr int STEADY = G * (S - 2);
+  static_assert(STEADY + NEPI + 1 < 64, "vmcnt allowance out of range");
+  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE + RS * 2048 + 4 * 32 * GROW * 4];
+  float* const sscale = reinterpret_cast<float*>(smem + S * STAGE);
+
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int tiles = tiles_m * tiles_n;
+  const int T = (tiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+  const int KT = K / kBK;  // a multiple of S, >= 2 * S (host)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int kh = lane >> 5;
+
+  auto coords = [&](int it, int& m0, int& n0) {
+    int tm, tn;
+    tile_coords<H3K_PIPE_GM>(static_cast<int>(blockIdx.x) + it * static_cast<int>(gridDim.x), tiles_m, tiles_n, tm, tn);
+    m0 = tm * BM;
+    n0 = tn * BN;
+  };
+
+  // ---------------------------------------------------------------- load streams
+  // Activations: buffer loads straight to LDS (one 32-bit row offset per load, the K position in a scalar).
+  // Weights: buffer loads into registers, issued as inline assembly -- see weight_load -- and covered by the
+  // explicit waits before each barrier.  The K loop carries few scalars: the next tile's origin is computed at tile
+  // start, not inside the loop.
+  const rsrc_t ra = make_rsrc(A, static_cast<uint32_t>(static_cast<int64_t>(M - 1) * lda + K));
+  const u32x4 rb = weight_rsrc(Bp, bp_bytes);
+  const uint32_t bvoff = static_cast<uint32_t>(lane) * 16u;
+  const uint32_t bstride = static_cast<uint32_t>(NBP) * kBlockBytes;  // one K-step of the packed grid
+  uint32_t aoff[DPW];   // this lane's 16-byte chunk of each of its DPW activation rows (K position 0)
+  uint32_t astep = 0;   // activations: K position of the next stage to load, in bytes
+  uint32_t bnext = 0;   // weights: offset of this wavefront's 4 blocks at the next K-step to load
+  uint32_t bfirst = 0;  // ... and at K-step 0 of the tile being loaded (a safe address for the tail loads)
+  auto point_loads = [&](int m0, int n0) {
+    // recomputed from an opaque lane index each time: kept from the prologue, these would be spilled
+    int l = static_cast<int>(threadIdx.x & 63);
+    __asm__ volatile("" : "+v"(l));
+    static_for<DPW>([&](auto i) {
+      const int r = (wave * DPW + i) * 16 + (l >> 2);  // (M - 1) * lda + K < 2^32 (host)
+      aoff[i] = static_cast<uint32_t>(min(m0 + r, M - 1)) * static_cast<uint32_t>(lda) +
+                static_cast<uint32_t>(swz_chunk(r, l & 3) * 16);
+    });
+    bfirst = static_cast<uint32_t>((n0 >> 5) + wn * WNB) * kBlockBytes;
+    bnext = bfirst;
+    astep = 0;
+  };
+  auto load_scales = [&](int slot, int m0, int n0) {  // waves 0 and 1: the tile's 256 xs / 256 s_ch
+    if (wave < 2) {
+      const float* p = wave == 0 ? xs + (min(m0 + 4 * lane, M - 4) & ~3) : sch + min(n0 + 4 * lane, N - 4);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(p), (lds_void*)(sscale + slot * 512 + wave * 256), 16,
+                                       0, 0);
+    }
+  };
+  // Every step issues the same G vector-memory ops: after the last step of the last tile the loads re-read K
+  // position 0 into a stage and registers nobody reads again, so the wait counts never depend on the path.
+  auto issue_a = [&](int stage, bool real) {
+    int8_t* dst = smem + stage * STAGE + wave * DPW * 1024;
+    const uint32_t k = real ? astep : 0u;
+    static_for<DPW>([&](auto i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(dst + i * 1024), 16, static_cast<int>(aoff[i]),
+                                                static_cast<int>(k), 0, 0);
+    });
+    astep += kBK;
+  };
+  v4i bq[S][WNB][2];  // weight fragments of S steps
+  auto issue_b = [&](auto u, bool real) {
+    const uint32_t b0 = real ? bnext : bfirst, b1 = b0 + 4096u;  // blocks 0-1 and 2-3: 12-bit immediate offsets
+    weight_load<0>(bq[u][0][0], rb, bvoff, b0);
+    weight_load<1024>(bq[u][0][1], rb, bvoff, b0);
+    weight_load<2048>(bq[u][1][0], rb, bvoff, b0);
+    weight_load<3072>(bq[u][1][1], rb, bvoff, b0);
+    weight_load<0>(bq[u][2][0], rb, bvoff, b1);
+    weight_load<1024>(bq[u][2][1], rb, bvoff, b1);
+    weight_load<2048>(bq[u][3][0], rb, bvoff, b1);
+    weight_load<3072>(bq[u][3][1], rb, bvoff, b1);
+    bnext += bstride;
+  };
+
+  // ---------------------------------------------------------------- fragments and MFMA
+  const int arow = wm * 128 + (lane & 31);
+  auto read_frags = [&](int stage, int half, v4i (&af)[WMB]) {
+    const int8_t* base = smem + stage * STAGE;
+    const int c = kh * 2 + half;  // the packed weight's k order: lanes 32-63 own the step's last 32 bytes
+    static_for<WMB>([&](auto i) { af[i] = *reinterpret_cast<const v4i*>(base + swz(arow + i * 32, c)); });
+  };
+  v16i acc[WMB][WNB];
+  auto zero_acc = [&]() { static_for<WMB>([&](auto i) { static_for<WNB>([&](auto j) { acc[i][j] = v16i{}; }); }); };
+  auto mfma = [&](const v4i (&af)[WMB], auto u, auto h) {
+    static_for<WMB>([&](auto i) {
+      static_for<WNB>([&](auto j) {
+        // weights as the first operand: each lane's accumulators hold one output row (see the epilogue)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bq[u][j][h], af[i], acc[i][j], 0, 0, 0);
+      });
+    });
+  };
+
+  // ---------------------------------------------------------------- epilogue
+  // Lane l owns output row m = cm0 + wm * 128 + i * 32 + (l & 31) (i < 4) and, per j < 4, the columns
+  // cn0 + wn * 128 + j * 32 + g * 8 + (l >> 5) * 4 + e (g, e < 4).
+  int cm0 = 0, cn0 = 0;
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  auto scaled = [&](int a, float x, float s) -> float {
+    return fp32_round_point(EAGER ? static_cast<float>(a) * fp32_round_point(x * s)
+                                  : fp32_round_point(static_cast<float>(a) * x) * s);
+  };
+  auto bits16 = [&](float f) -> uint32_t { return ODT == H3K_F16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f); };
+  auto pack4 = [&](const float (&f)[4]) -> uint2 {
+    if (ODT == H3K_BF16) {
+      const bf16x2 lo = __builtin_convertvector((f32x2){f[0], f[1]}, bf16x2);
+      const bf16x2 hi = __builtin_convertvector((f32x2){f[2], f[3]}, bf16x2);
+      return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    }
+    return make_uint2(bits16(f[0]) | (bits16(f[1]) << 16), bits16(f[2]) | (bits16(f[3]) << 16));
+  };
+
+  // Stores the finished tile; true when exactly NEPI vector-memory ops were issued (the full-tile 16-bit path).
+  // One path computes every value: per 32-row block, the wavefront writes its fp32 results (and, if asked, the raw
+  // accumulators) into its staging area and reads them back row-contiguous.  Full tiles with 16-bit, line-aligned
+  // outputs then store 8 outputs per lane, whole 128-byte lines, non-temporally; everything else (tiles cut by M or
+  // N, bias, accumulator dump, fp32 or unaligned outputs) stores 4 per lane, predicated on M and N, after waiting for
+  // every load in flight -- the next tile's weight fragments included, so nothing in flight can be spilled there.
+  // A single path keeps the accumulator reads to one block at a time (two paths made the compiler read all 256
+  // ahead of the branch and spill).  The xs slot holds whole 16-byte chunks only where they lie inside [0, M), so a
+  // tile cut by M reads xs itself.
+  auto epilogue = [&](int slot) -> bool {
+    // lane- and tile-derived values recomputed from opaque copies: shared with the K loop's address arithmetic
+    // they would stay live across it
+    int lane = static_cast<int>(threadIdx.x & 63);
+    __asm__ volatile("" : "+v"(lane));
+    const int kh = lane >> 5;
+    const int row0 = cm0 + wm * 128 + (lane & 31);
+    const int col0 = cn0 + wn * 128 + kh * 4;
+    const float* const sx = sscale + slot * 512;
+    const bool full = cm0 + BM <= M && cn0 + BN <= N && vec_out && !ACC && bias == nullptr;
+    const bool lines = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (ldo & 7) == 0;
+    const bool fast = full && STAGED && lines;
+    if (!fast) {
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<0>();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    float* const stg = reinterpret_cast<float*>(smem + S * STAGE + RS * 2048) + wave * (32 * GROW);
+    const bool cut_m = cm0 + BM > M;
+    static_for<WMB>([&](auto i) {
+      static_for<2>([&](auto pass) {  // 0: outputs, 1: accumulators (acc_out)
+        if (pass == 1 && !ACC) return;
+        __builtin_amdgcn_sched_barrier(0);
+        const float x = cut_m ? xs[min(row0 + i * 32, M - 1)] : sx[row0 - cm0 + i * 32];
+        float* const w = stg + (lane & 31) * GROW + kh * 4;
+        static_for<WNB>([&](auto j) {
+          static_for<4>([&](auto g) {
+            // element reads of the scale slot: a 16-byte LDS read here makes the compiler drain vmcnt
+            const float* p = sx + 256 + col0 - cn0 + j * 32 + g * 8;
+            float4 v;
+            if (pass == 0) {
+              v = make_float4(scaled(acc[i][j][g * 4 + 0], x, p[0]), scaled(acc[i][j][g * 4 + 1], x, p[1]),
+                              scaled(acc[i][j][g * 4 + 2], x, p[2]), scaled(acc[i][j][g * 4 + 3], x, p[3]));
+            } else {
+              v = make_float4(__int_as_float(acc[i][j][g * 4 + 0]), __int_as_float(acc[i][j][g * 4 + 1]),
+                              __int_as_float(acc[i][j][g * 4 + 2]), __int_as_float(acc[i][j][g * 4 + 3]));
+            }
+            *reinterpret_cast<float4*>(w + j * 32 + g * 8) = v;
+          });
+        });
+        wave_lds_sync();
+        if (fast) {
+          static_for<8>([&](auto q) {  // 4 rows x 256 bytes per store instruction
+            const int rr = q * 4 + (lane >> 4);
+            const float* rp = stg + rr * GROW + (lane & 15) * 8;
+            const float4 lo = *reinterpret_cast<const float4*>(rp), hi = *reinterpret_cast<const float4*>(rp + 4);
+            const uint2 a = pack4({lo.x, lo.y, lo.z, lo.w}), b = pack4({hi.x, hi.y, hi.z, hi.w});
+            u32x4* dst = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) +
+                                                  static_cast<int64_t>(cm0 + wm * 128 + i * 32 + rr) * ldo + cn0 +
+                                                  wn * 128 + (lane & 15) * 8);
+            __builtin_nontemporal_store(u32x4{a.x, a.y, b.x, b.y}, dst);
+          });
+        } else {
+          const int r2 = lane >> 5, c4 = (lane & 31) * 4;  // rows r2 + 2q, columns c4 .. c4 + 3 of the block
+          const int n = cn0 + wn * 128 + c4;
+          static_for<16>([&](auto q) {
+            const int m = cm0 + wm * 128 + i * 32 + r2 + 2 * q;
+            const float4 v = *reinterpret_cast<const float4*>(stg + (r2 + 2 * q) * GROW + c4);
+            if (m < M) {
+              const float f[4] = {v.x, v.y, v.z, v.w};
+              if (pass == 1) {
+                int32_t* dst = acc_out + static_cast<int64_t>(m) * N + n;
+                static_for<4>([&](auto e) {
+                  if (n + e < N) dst[e] = __float_as_int(f[e]);
+                });
+              } else {
+                float o[4];
+                static_for<4>([&](auto e) {
+                  float y = f[e];
+                  if (ODT != H3K_F32) y = ODT == H3K_F16 ? round_f16(y) : round_bf16(y);
+                  if (bias && n + e < N) {  // added after the output rounding (qlinear.py:404-405)
+                    float b;
+                    if (ODT == H3K_F32) b = static_cast<const float*>(bias)[n + e];
+                    else if (ODT == H3K_F16) b = f16_to_f32(static_cast<const uint16_t*>(bias)[n + e]);
+                    else b = bf16_to_f32(static_cast<const uint16_t*>(bias)[n + e]);
+                    y = ODT == H3K_F32 ? y + b : fp32_round_point(y + b);
+                  }
+                  o[e] = y;
+                });
+                const int64_t off = static_cast<int64_t>(m) * ldo + n;
+                if (n + 3 < N && vec_out) {
+                  if (ODT == H3K_F32)
+                    *reinterpret_cast<float4*>(static_cast<float*>(out) + off) = make_float4(o[0], o[1], o[2], o[3]);
+                  else
+                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + off) =
+                        make_uint2(bits16(o[0]) | (bits16(o[1]) << 16), bits16(o[2]) | (bits16(o[3]) << 16));
+                } else {
+                  static_for<4>([&](auto e) {
+                    if (n + e < N) {
+                      if (ODT == H3K_F32) static_cast<float*>(out)[off + e] = o[e];
+                      else static_cast<uint16_t*>(out)[off + e] = static_cast<uint16_t>(bits16(o[e]));
+                    }
+                  });
+                }
+              }
+            }
+          });
+        }
+        wave_lds_sync();  // the next block overwrites the staging area
+      });
+    });
+    if (!fast) wait_vmcnt<0>();  // nothing of unknown count stays pending into the next tile's first steps
+    return fast;
+  };
+
+  // ---------------------------------------------------------------- prologue
+  coords(0, cm0, cn0);
+  point_loads(cm0, cn0);
+  load_scales(0, cm0, cn0);
+  static_for<S>([&](auto s) {
+    issue_a(s, true);
+    issue_b(s, true);
+  });
+  wait_vmcnt<G * (S - 1)>();
+  lds_barrier();
+  zero_acc();
+
+  v4i a0[WMB], a1[WMB];
+  read_frags(0, 0, a0);
+  bool exact = false;  // the last epilogue issued exactly NEPI vector-memory ops
+  for (int it = 0; it < T; ++it) {
+    const bool has_next = it + 1 < T;
+    int nm0 = 0, nn0 = 0;  // the next tile's origin
+    if (has_next) coords(it + 1, nm0, nn0);
+    if (it > 0) load_scales(it % RS, cm0, cn0);
+    for (int kt0 = 0; kt0 < KT; kt0 += S) {
+      static_for<S>([&](auto u) {
+        const int kt = kt0 + u;
+        const bool last = kt == KT - 1;
+        const bool more = has_next || kt < KT - S;  // step kt + S exists (this tile's or the next one's)
+        if (kt == KT - S && has_next) point_loads(nm0, nn0);  // the load streams move on to the next tile
+        read_frags(u, 1, a1);
+        mfma(a0, u, std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        // step kt + 1 must have landed: normally S - 2 newer steps may still be in flight; in the S - 1 steps after
+        // an epilogue its stores (and waves 0-1's scale load) sit in between; in the last tile's last steps wait for
+        // everything
+        if (it > 0 && kt < S - 1) {
+          if (exact) wait_vmcnt<STEADY + NEPI>();
+          else wait_vmcnt<0>();
+        } else if (!has_next && kt >= KT - S) {
+          wait_vmcnt<0>();
+        } else {
+          wait_vmcnt<STEADY>();
+        }
+        lds_barrier();
+        issue_a(u, more);  // stage kt + S into the stage just read
+        if (!last) read_frags((u + 1) % S, 0, a0);
+        mfma(a1, u, std::integral_constant<int, 1>{});
+        issue_b(u, more);  // weight fragments of step kt + S into the registers just consumed
+      });
+    }
+    exact = epilogue(it % RS);
+    zero_acc();
+    if (has_next) {
+      read_frags(0, 0, a0);
+      cm0 = nm0;
+      cn0 = nn0;
+    }
+  }
+  wait_vmcnt<0>();  // no direct-to-LDS write may land after the workgroup has ended
+}
+
+#ifndef H3K_W8P_S
+#define H3K_W8P_S 4
+#endif
+
+template <int ODT, bool EAGER, bool ACC>
+static void launch(const int8_t* a, int64_t lda, const int8_t* bp, uint32_t bp_bytes, int nbp, int m, int n, int k,
+                   const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, int grid,
+                   hipStream_t st) {
+  const size_t es = ODT == H3K_F32 ? 4 : 2;
+  const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
+  hipLaunchKernelGGL((gemm_w8p_kernel<H3K_W8P_S, ODT, EAGER, ACC>), dim3(grid), dim3(256), 0, st, a, lda, bp, bp_bytes,
+                     nbp, m, n, k, xs, sch, bias, out, ldo, acc, vec_out);
+}
+
+// ------------------------------------------------------------------------------------------ packing
+// Row-major int8 grid [n, k] -> packed layout.  One thread per 16-byte fragment chunk, in packed order: a
+// wavefront's stores are 1 KiB contiguous.  Rows past n are written as zeros.
+__global__ __launch_bounds__(256) void pack_w8_kernel(const int8_t* __restrict__ w8, int64_t ldw, int n, int nbp,
+                                                      int8_t* __restrict__ wp, int64_t chunks) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (u >= chunks) return;
+  const int l = static_cast<int>(u & 63);
+  const int64_t frag = u >> 6;  // (t * NBP + b) * 2 + h
+  const int h = static_cast<int>(frag & 1);
+  const int64_t tb = frag >> 1;
+  const int b = static_cast<int>(tb % nbp);
+  const int t = static_cast<int>(tb / nbp);
+  const int row = b * 32 + (l & 31);
+  u32x4 v = u32x4{0u, 0u, 0u, 0u};
+  if (row < n) v = *reinterpret_cast<const u32x4*>(w8 + static_cast<int64_t>(row) * ldw + t * 64 + (l >> 5) * 32 + h * 16);
+  *reinterpret_cast<u32x4*>(wp + u * 16) = v;
+}
+
+}  // namespace w8p
+
+int cu_count();
+
+// Bytes of the packed grid of an [n, k] weight (n padded to a multiple of 256: a whole output tile).
+int64_t w8p_bytes(int64_t n, int64_t k) { return (n + 255) / 256 * 256 * k; }
+
+// Whether gemm_w8p_launch serves this shape: K a multiple of 64 * S with at least 2 * S steps (the per-tile step
+// phases must not overlap), M >= 4, and the same tile-count rule as the row-major persistent kernel (at least 5/8
+// of the CUs get a 256 x 256 tile, and the last round of tiles is not mostly idle).
+bool w8p_serves(int64_t m, int64_t n, int64_t k) {
+  constexpr int S = H3K_W8P_S;
+  if (k % (64 * S) || k < 2 * S * 64 || m < 4 || n < 4 || n % 4 || m > (1 << 30) || n > (1 << 30) || k > (1 << 17)) return false;
+  if (w8p_bytes(n, k) >= (int64_t(1) << 32)) return false;
+  const int cus = cu_count();
+  const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256), tiles128x256 = ((m + 127) / 128) * ((n + 255) / 256);
+  auto fill = [cus](int64_t t) { return static_cast<double>(t) / (static_cast<double>((t + cus - 1) / cus) * cus); };
+  return m > 512 && tiles256 >= cus * 5 / 8 && fill(tiles256) >= 0.83 * fill(tiles128x256);
+}
+
+// Preconditions (checked by the caller): w8p_serves(m, n, k); a and w8p 16-byte aligned, lda a multiple of 16;
+// xs, s_ch and bias 16-byte aligned.
+void gemm_w8p_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
+                     const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo, int32_t* acc_out,
+                     hipStream_t st) {
+  const int tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  const int grid = tiles < cu_count() ? tiles : cu_count();
+  const uint32_t bytes = static_cast<uint32_t>(w8p_bytes(n, k));
+  const int nbp = static_cast<int>((n + 255) / 256 * 8);
+  const bool e = mode == H3K_MODE_EAGER;
+#define H3K_L(D, E, C) w8p::launch<D, E, C>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid, st)
+  if (acc_out) {  // the accumulator dump: its own instantiations (a second read of every accumulator costs registers)
+    if (odt == H3K_BF16) { if (e) H3K_L(H3K_BF16, true, true); else H3K_L(H3K_BF16, false, true); }
+    else if (odt == H3K_F16) { if (e) H3K_L(H3K_F16, true, true); else H3K_L(H3K_F16, false, true); }
+    else { if (e) H3K_L(H3K_F32, true, true); else H3K_L(H3K_F32, false, true); }
+  } else {
+    if (odt == H3K_BF16) { if (e) H3K_L(H3K_BF16, true, false); else H3K_L(H3K_BF16, false, false); }
+    else if (odt == H3K_F16) { if (e) H3K_L(H3K_F16, true, false); else H3K_L(H3K_F16, false, false); }
+    else { if (e) H3K_L(H3K_F32, true, false); else H3K_L(H3K_F32, false, false); }
+  }
+#undef H3K_L
+}
+
+}  // namespace h3k
+
+using namespace h3k;
+
+extern "C" int64_t h3k_w8_packed_bytes(int64_t n, int64_t k) {
+  if (n < 0 || k < 0 || k % 64) return -1;
+  return w8p_bytes(n, k);
+}
+
+extern "C" int h3k_gemm_packed_serves(int64_t m, int64_t n, int64_t k) { return w8p_serves(m, n, k) ? 1 : 0; }
+
+extern "C" int h3k_pack_w8(const int8_t* w8, int64_t ldw, int64_t n, int64_t k, int8_t* w8p, void* stream) {
+  if (n < 0 || k <= 0 || k % 64 || k > (1 << 30) || n > (1 << 30)) return fail(H3K_EINVAL, "pack: bad n=%lld k=%lld (k a multiple of 64)", (long long)n, (long long)k);
+  if (ldw < k) return fail(H3K_EINVAL, "row stride smaller than the rows");
+  if (n == 0) return H3K_OK;
+  if (!w8 || !w8p) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(w8, 16) || ldw % 16 || !aligned(w8p, 16)) return fail(H3K_EINVAL, "pack: 16-byte alignment needed");
+  const int64_t chunks = w8p_bytes(n, k) / 16;
+  hipLaunchKernelGGL(w8p::pack_w8_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), w8, ldw, static_cast<int>(n),
+                     static_cast<int>((n + 255) / 256 * 8), w8p, chunks);
+  return check_launch("pack_w8");
+}
+
+extern "C" int h3k_gemm_a8w8_packed(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
+                                    const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out,
+                                    int out_dtype, int64_t ldo, int32_t* acc_out, void* stream) {
+  if (m < 0 || n < 0 || k < 0) return fail(H3K_EINVAL, "bad GEMM shape");
+  if (mode != H3K_MODE_CK && mode != H3K_MODE_EAGER) return fail(H3K_EINVAL, "mode must be ck (0) or eager (1)");
+  if (out_dtype != H3K_BF16 && out_dtype != H3K_F16 && out_dtype != H3K_F32)
+    return fail(H3K_EINVAL, "out dtype code %d unsupported", out_dtype);
+  if (m == 0 || n == 0) return H3K_OK;
+  if (!w8p_serves(m, n, k))
+    return fail(H3K_EINVAL, "the packed-weight GEMM does not serve m=%lld n=%lld k=%lld (h3k_gemm_packed_serves)",
+                (long long)m, (long long)n, (long long)k);
+  if (lda < k || ldo < n) return fail(H3K_EINVAL, "row strides smaller than the rows");
+  if ((m - 1) * lda + k >= (int64_t(1) << 32)) return fail(H3K_EINVAL, "a spans 4 GiB or more (one buffer descriptor)");
+  if (!a || !xs || !w8p || !s_ch || !out) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(a, 16) || lda % 16 || !aligned(w8p, 16))
+    return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
+  if (!aligned(xs, 16) || !aligned(s_ch, 16) || (bias && !aligned(bias, 16)))
+    return fail(H3K_EINVAL, "xs, s_ch and bias must be 16-byte aligned");
+  gemm_w8p_launch(a, lda, xs, w8p, s_ch, bias, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), mode, out,
+                  out_dtype, ldo, acc_out, static_cast<hipStream_t>(stream));
+  return check_launch("gemm_a8w8_packed");
+}

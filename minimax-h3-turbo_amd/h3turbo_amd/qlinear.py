@@ -175,6 +175,16 @@ def _decode(dw: _DevWeight, group: int) -> torch.Tensor:
     return w8
 
 
+def _decode_packed(dw: _DevWeight, group: int) -> torch.Tensor:
+    """The grid in the packed layout of the large-shape GEMM (h3k_decode_w4_packed): a flat int8 buffer."""
+    lib = _lib.load()
+    w8p = torch.empty(lib.h3k_w8_packed_bytes(dw.n, dw.k), dtype=torch.int8, device=dw.q.device)
+    _lib.check(lib.h3k_decode_w4_packed(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(),
+                                        dw.n, dw.k, group, w8p.data_ptr(), _lib.stream_of(dw.q.device)),
+               "h3k_decode_w4_packed")
+    return w8p
+
+
 @torch.no_grad()
 def decode_int8_grid(w: W4A8Weight) -> torch.Tensor:
     """int8 [N, K]: the exact grid the int8 GEMM consumes (qlinear.py:194-204)."""
@@ -269,16 +279,27 @@ class _HipRunner:
         self.ocode = _lib.act_code(out_dtype)
         self.bias = None if bias is None else bias.to(device=w.q.device, dtype=out_dtype).contiguous()
         self._w8: Optional[torch.Tensor] = None
+        self._w8p: Optional[torch.Tensor] = None
         self.lib = _lib.load()
         g = w.group_size
-        self.few_rows_ok = (self.k % 64 == 0 and (g in (16, 32) or g % 64 == 0) and self.k % g == 0
-                            and self.dw.q.data_ptr() % 16 == 0 and self.dw.ldq % 16 == 0)
+        q_lines = self.dw.q.data_ptr() % 16 == 0 and self.dw.ldq % 16 == 0
+        self.few_rows_ok = self.k % 64 == 0 and (g in (16, 32) or g % 64 == 0) and self.k % g == 0 and q_lines
+        self.packed_ok = (q_lines and self.k % 64 == 0 and self.dw.s_ch.data_ptr() % 16 == 0
+                          and (self.bias is None or self.bias.data_ptr() % 16 == 0))
 
     @property
     def w8(self) -> torch.Tensor:
+        """The row-major int8 grid, decoded once per call when first needed."""
         if self._w8 is None:
             self._w8 = _decode(self.dw, self.w.group_size)
         return self._w8
+
+    @property
+    def w8p(self) -> torch.Tensor:
+        """The packed int8 grid of the large-shape GEMM, decoded once per call when first needed."""
+        if self._w8p is None:
+            self._w8p = _decode_packed(self.dw, self.w.group_size)
+        return self._w8p
 
     def __call__(self, x2: torch.Tensor, out: torch.Tensor, act: Optional[str] = None) -> None:
         if self.precision == "a8":
@@ -313,6 +334,13 @@ class _HipRunner:
                                               dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
                                               _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0),
                                               _lib.ptr(ws), None, _lib.stream_of(xq.device)), "h3k_gemm_w4a8")
+            return
+        if (self.packed_ok and xs.data_ptr() % 16 == 0 and out.stride(0) >= self.n
+                and self.lib.h3k_gemm_packed_serves(m, self.n, self.k)):
+            _lib.check(self.lib.h3k_gemm_a8w8_packed(xq.data_ptr(), self.k, xs.data_ptr(), self.w8p.data_ptr(),
+                                                     self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
+                                                     _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0),
+                                                     None, _lib.stream_of(xq.device)), "h3k_gemm_a8w8_packed")
             return
         _lib.check(self.lib.h3k_gemm_a8w8(xq.data_ptr(), self.k, xs.data_ptr(), self.w8.data_ptr(), self.k,
                                           self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,

@@ -149,12 +149,14 @@ def mlp_ref(h: torch.Tensor, w: Dict[str, object], act: str, mode: str = "ck") -
 
 def block_ref(x: torch.Tensor, w: Dict[str, object], mods: Sequence[torch.Tensor], segments, cos: torch.Tensor,
               sin: torch.Tensor, heads: int, head_dim: int, act: str, eps: float, qk_eps: float,
-              rope_impl: str = "torch", mode: str = "ck", attend: Optional[torch.Tensor] = None) -> torch.Tensor:
+              rope_impl: str = "torch", mode: str = "ck", attend: Optional[torch.Tensor] = None,
+              modulated: Optional[Sequence[torch.Tensor]] = None) -> torch.Tensor:
     """The reference block (model.py:234-242) on the CPU in x.dtype; returns the new residual (x is not mutated).
 
     attend: an attention output [S, heads * head_dim] (before the out projection) to use in place of the one
-    attend_ref computes -- the GPU's own SDPA result, so that a comparison isolates everything but the attention
-    kernel."""
+    attend_ref computes; modulated: the two RMSNorm + modulation outputs (before attention, before the MLP) to use
+    in place of the ones computed here.  With a GPU block's own values of those two steps -- whose reduction orders
+    are not the reference's -- a comparison covers every other step exactly."""
     x = x.clone()
     dt = x.dtype
     sh_a, sc_a, g_a, sh_m, sc_m, g_m = mods
@@ -164,12 +166,12 @@ def block_ref(x: torch.Tensor, w: Dict[str, object], mods: Sequence[torch.Tensor
             x[a:b].addcmul_(y[a:b], gate[r].to(dt))
 
     rmsn = lambda v, g: F.rms_norm(v, (v.shape[-1],), g.to(v.dtype), eps)  # noqa: E731
-    h = _modulate(rmsn(x, w["norm1"]), sh_a, sc_a, segments)
+    h = _modulate(rmsn(x, w["norm1"]), sh_a, sc_a, segments) if modulated is None else modulated[0].to(dt)
     if attend is None:
         gate_add(attention_ref(h, w, cos, sin, heads, head_dim, qk_eps, rope_impl, mode), g_a)
     else:
         gate_add(_linear(attend.to(dt), w["out"], mode=mode), g_a)
-    h = _modulate(rmsn(x, w["norm2"]), sh_m, sc_m, segments)
+    h = _modulate(rmsn(x, w["norm2"]), sh_m, sc_m, segments) if modulated is None else modulated[1].to(dt)
     gate_add(mlp_ref(h, w, act, mode), g_m)
     return x
 

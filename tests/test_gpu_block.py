@@ -113,18 +113,17 @@ def _random_w4a8_parts(n, k, g):
 def test_config4_width_block_within_the_north_star_tolerance(act):
     """The config-4 block width (hidden 5120, 40 x 128 heads, FFN 13824) against the CPU block oracle at S = 384.
 
-    north_star's bar is max|out - ref| <= 1e-2 * RMS(ref) on the bf16 output.  It is asserted with the oracle given
-    the GPU's own attention-kernel output (PyTorch-ROCm SDPA, which north_star leaves out of the hand-written path),
-    so the comparison covers every other step of the block: the RMSNorm + modulation, the q/k/v projection, the
-    out projection, both gated residual adds and the MLP.  The output is the residual stream rounded to bf16, whose
-    spacing at |out| >= 2 (2^-6 = 0.0156) is already above 1e-2 of an RMS near 1, and the fused RMSNorm's own
-    summation order moves a few modulated inputs by one ulp; each element is therefore held to the larger of
-    1e-2 * RMS and one bf16 step of the reference value (measured: at most one step, rel-L2 3-6e-4).  The attention
-    prologue (q/k/v projection, q/k norm + rope) is held bit-exact on the GPU's own modulated input.
+    north_star's bar, max|out - ref| <= 1e-2 * RMS(ref) on the bf16 output, is asserted with the oracle given the
+    GPU's own results of the two steps whose arithmetic order is not the reference's: the attention kernel
+    (PyTorch-ROCm SDPA, outside the hand-written path) and the fused RMSNorm + modulation (its sum of squares runs
+    in its own order; test_fused_rms_modulate_matches_the_torch_ops holds it within one bf16 ulp).  Everything else
+    -- the four W4A8 linears, the q/k norm + rope, the gated residual adds, the activation -- must then agree; the
+    attention prologue (q/k/v after norm + rope) is also held bit-exact.
 
-    Against the oracle's own fp32 attention the block differs by SDPA's bf16 numerics (P rounded to bf16 before
-    P.V), amplified by the two int8 requantisations downstream: measured max-abs 0.06 (GELU) and 0.11 (SwiGLU) of
-    RMS, rel-L2 0.4-0.6 % of the residual.  That comparison is reported and held to rel-L2 1e-2."""
+    The fully independent comparison (oracle norms and fp32 attention) is reported and held to rel-L2 1e-2: SDPA's
+    bf16 numerics (P rounded to bf16 before P.V) and one-ulp norm differences move individual int8 activations by a
+    quantisation step, and the two requantisations downstream amplify that -- measured max-abs 0.06 (GELU) and
+    0.11 (SwiGLU) of RMS at rel-L2 0.4-0.6 %."""
     s, hidden, heads, hd, ffn = 384, 5120, 40, 128, 13824
     print(f"config-4-width block act={act} S={s}", flush=True)
     g = torch.Generator().manual_seed(404 + (act == "swiglu"))
@@ -142,39 +141,42 @@ def test_config4_width_block_within_the_north_star_tolerance(act):
            "fc1": _random_w4a8_parts(cfg.fc1_out, hidden, g), "fc2": _random_w4a8_parts(hidden, ffn, g)}
     w = block_weights_gpu(lin, norms)
     blk = bk.DiTBlock(cfg)
-    seen = {}
-    real_sdpa = bk._sdpa
+    seen = {"h": []}
+    real_sdpa, real_rms_modulate = bk._sdpa, bk.rms_modulate
 
     def capture_sdpa(q, k, v):  # the attention kernel's inputs and output, as the block ran them
         o = real_sdpa(q, k, v)
         seen.update(q=q[0].cpu(), k=k[0].cpu(), v=v[0].cpu(), o=o[0].cpu())
         return o
 
-    bk._sdpa = capture_sdpa
+    def capture_rms_modulate(*a, **kw):  # the two RMSNorm + modulation outputs
+        h = real_rms_modulate(*a, **kw)
+        seen["h"].append(h.cpu())
+        return h
+
+    bk._sdpa, bk.rms_modulate = capture_sdpa, capture_rms_modulate
     try:
         out = blk(x.to(DEV), w, [m.to(DEV) for m in mods], segs_gpu(segs), (cos.to(DEV), sin.to(DEV))).cpu()
     finally:
-        bk._sdpa = real_sdpa
+        bk._sdpa, bk.rms_modulate = real_sdpa, real_rms_modulate
+    assert len(seen["h"]) == 2
     mlp = blk.mlp(x.to(DEV), w).cpu()
     print("  GPU block done; CPU oracle running", flush=True)
     ref_w = {**lin, **norms}
     o_gpu = seen["o"].transpose(0, 1).reshape(s, heads * hd)  # [heads, S, D] -> [S, heads * D]
-    want = br.block_ref(x, ref_w, mods, segs, cos, sin, heads, hd, act, 1e-5, 1e-5, attend=o_gpu)
+    want = br.block_ref(x, ref_w, mods, segs, cos, sin, heads, hd, act, 1e-5, 1e-5, attend=o_gpu, modulated=seen["h"])
     full = br.block_ref(x, ref_w, mods, segs, cos, sin, heads, hd, act, 1e-5, 1e-5)
 
     # the attention prologue on the GPU's own modulated input: q, k, v bit for bit
-    h_gpu = bk.rms_modulate(x.to(DEV), w.norm1, mods[0].to(DEV), mods[1].to(DEV), 1e-5, segs_gpu(segs)).cpu()
-    h_ref = br._modulate(F.rms_norm(x, (hidden,), norms["norm1"].to(x.dtype), 1e-5), mods[0], mods[1], segs)
-    qkv = br._linear(h_gpu, lin["qkv"])
+    qkv = br._linear(seen["h"][0], lin["qkv"])
     q, k, v = (t.reshape(s, heads, hd).clone() for t in qkv.split(heads * hd, dim=-1))
     br.norm_rope_ref(q, k, norms["q_norm"], norms["k_norm"], 1e-5, cos, sin, "torch")
+    h_ref = br._modulate(F.rms_norm(x, (hidden,), norms["norm1"].to(x.dtype), 1e-5), mods[0], mods[1], segs)
 
     err = (out.double() - want.double()).abs()
     rms = want.double().pow(2).mean().sqrt().item()
     report = dict(max_abs_over_rms=err.max().item() / rms, out_rel=rel(out, want),
-                  beyond_1e2_rms=int((err > 1e-2 * rms).sum()), beyond_one_bf16_step=int((err > bf16_ulp(want)).sum()),
-                  modulated_input_ulps=int((h_gpu != h_ref).sum()),
-                  update_rel=rel(out.double() - x.double(), want.double() - x.double()),
+                  modulated_input_ulps=int((seen["h"][0] != h_ref).sum()),
                   full_chain_max_abs_over_rms=(out.double() - full.double()).abs().max().item() / rms,
                   full_chain_rel=rel(out, full), mlp_ns=within_north_star(mlp, mlp_ref := br.mlp_ref(x, ref_w, act))[1],
                   mlp_rel=rel(mlp, mlp_ref))
@@ -182,9 +184,7 @@ def test_config4_width_block_within_the_north_star_tolerance(act):
     assert torch.equal(seen["q"].transpose(0, 1), q) and torch.equal(seen["k"].transpose(0, 1), k)
     assert torch.equal(seen["v"].transpose(0, 1), v)
     assert within_north_star(mlp, mlp_ref)[0], "MLP sub-path beyond 1e-2 * RMS"
-    bound = torch.maximum(torch.full_like(err, 1e-2 * rms), bf16_ulp(want))
-    assert (err <= bound).all(), "block beyond max(1e-2 * RMS, one bf16 step) of the oracle on the same attention"
-    assert report["out_rel"] < 2e-3
+    assert report["max_abs_over_rms"] <= 1e-2, "block beyond 1e-2 * RMS of the oracle on the same attention and norms"
     assert report["full_chain_rel"] < 1e-2
 
 

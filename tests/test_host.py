@@ -46,7 +46,15 @@ def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     # workspace too small
     assert lib.h3k_w4a8_linear(None, 0, 4, 256, 256, None, 128, None, 3, 16, None, None, 8, 16, 256, None, 0, None, 0, 8,
                                None, 0, None) == _lib.ESPACE
-    assert lib.h3k_w4a8_linear_workspace(4, 8, 256) == 1024 + 256 + 2048
+    # int8 activations + scales + the weight region: the decoded grid with n rounded up to 256 rows (the packed
+    # layout's padding), or the few-row GEMM's accumulators if larger
+    assert lib.h3k_w4a8_linear_workspace(4, 8, 256) == 1024 + 256 + 256 * 256
+    assert lib.h3k_w4a8_linear_workspace(600, 13824, 5120) == 600 * 5120 + 2560 + 13824 * 5120
+    # the packed grid's size and the shapes its GEMM serves
+    assert lib.h3k_w8_packed_bytes(33, 128) == 256 * 128 and lib.h3k_w8_packed_bytes(32, 100) == -1
+    assert lib.h3k_gemm_packed_serves(32768, 13824, 5120) == 1 and lib.h3k_gemm_packed_serves(512, 13824, 5120) == 0
+    assert lib.h3k_gemm_a8w8_packed(None, 5120, None, None, None, None, 512, 13824, 5120, 0, None, _lib.BF16, 13824, None,
+                                    None) == _lib.EINVAL
     # empty work is a no-op
     assert lib.h3k_rotate_quant(None, _lib.BF16, 0, 256, 256, 256, 0, None, 256, None, None) == 0
     # split norm + rope: head_dim outside {32, 64, 128, 256}; overlapping head-major outputs
