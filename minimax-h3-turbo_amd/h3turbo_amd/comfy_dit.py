@@ -25,7 +25,7 @@ import torch
 
 from .engine import H3Engine
 from .h3t import H3TFile
-from .stream import _DEVICE_MARGIN, plan_residency
+from .stream import HBM_MARGIN, plan_residency
 
 LOG = logging.getLogger("h3turbo_amd")
 ACT_MIB_PER_TOKEN = 0.18  # activation peak of an unchunked forward, MiB per token (bf16)
@@ -118,7 +118,7 @@ class H3TurboDiT(torch.nn.Module):
     def _resident_for(self, budget: int) -> int:
         if self.resident_blocks:
             return int(self.resident_blocks)
-        return plan_residency(self.store, budget, int(0.25 * 2 ** 30) + _DEVICE_MARGIN, RING)
+        return plan_residency(self.store, budget, int(0.25 * 2 ** 30) + HBM_MARGIN, RING)
 
     def ensure_loaded(self, budget: Optional[int] = None) -> int:
         """Build the engine inside `budget` bytes of device memory (default: what is free now), or bring a parked

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from h3turbo_amd.blockstore import BlockLayout, HostBlockStore, block_tensors
-from h3turbo_amd.stream import ACQUIRED, PENDING, StreamingProvider, free_ram_bytes, plan_pinned_blocks, plan_residency
+from h3turbo_amd.stream import StreamingProvider, free_ram_bytes, plan_pinned_blocks, plan_residency
 from h3turbo_amd.types import BlockWeights, W4A8Weight
 
 LAYERS = 6
@@ -80,7 +80,7 @@ def forward(p, store, compute=None, check=True):
 
 
 def no_slot_held(p):
-    return all(s.state != ACQUIRED for s in p._slots)
+    return all(not s.held for s in p._slots)
 
 
 # ------------------------------------------------------------------------------------------------ block store
@@ -226,9 +226,14 @@ def test_no_slot_is_written_while_the_model_holds_it(store):
 
     def hook(dst, src, nb):
         assert ready.wait(10)
-        slot = next(s for s in holder["p"]._slots if s.buf is dst)
-        assert slot.state == PENDING, f"copy into a slot in state {slot.state}"
-        log.append(slot.idx)
+        p = holder["p"]
+        slot = next(s for s in p._slots if s.buf is dst)
+        b = next(b for b in range(LAYERS) if p.store.block_tensor(b).data_ptr() == src.data_ptr())
+        # a copy writes only the block its slot is assigned to, and a held slot only while its acquire() still waits
+        # for this very fill (the model has not been handed the weights yet)
+        assert slot.block == b, f"copy of block {b} into slot {slot.index} assigned to block {slot.block}"
+        assert not slot.held or not slot.ticket.done(), f"copy into slot {slot.index} while the model reads it"
+        log.append(slot.index)
         time.sleep(0.003)
         dst.copy_(src)
 
@@ -240,7 +245,7 @@ def test_no_slot_is_written_while_the_model_holds_it(store):
         expect = [raw(t) for w in held for t in tensors_of(w)]
         time.sleep(0.15)
         assert [raw(t) for w in held for t in tensors_of(w)] == expect
-        assert sum(s.state == ACQUIRED for s in p._slots) == 2
+        assert sum(s.held for s in p._slots) == 2
         with pytest.raises(RuntimeError, match="already acquired"):
             p.acquire(0)
         third = p.acquire(2)
@@ -338,7 +343,7 @@ def test_worker_error_surfaces_and_provider_still_closes(store):
         for _ in range(3):
             forward(p, store, check=False)
     p.close()
-    assert not p._thread.is_alive()
+    assert not p._engine.thread.is_alive()
 
 
 def test_wait_timeout_reports_state(store):
@@ -361,7 +366,7 @@ def test_wait_timeout_reports_state(store):
 def test_close_is_idempotent_joins_and_blocks_further_use(store):
     p = StreamingProvider(store, "cpu", resident=1, prefetch=2, ring=2, pin=True)
     forward(p, store)
-    th = p._thread
+    th = p._engine.thread
     p.close()
     p.close()
     assert not th.is_alive()
@@ -372,7 +377,7 @@ def test_close_is_idempotent_joins_and_blocks_further_use(store):
 
 def test_all_resident_needs_no_worker(store):
     with StreamingProvider(store, "cpu", resident=LAYERS) as p:
-        assert p._thread is None and p.stats()["slots"] == 0
+        assert p._engine is None and p.stats()["slots"] == 0
         forward(p, store)
         forward(p, store)
 
