@@ -50,11 +50,14 @@ extern "C" int h3k_version(void) { return 2; }
 
 extern "C" const char* h3k_last_error(void) { return g_last_error.c_str(); }
 
+// Calls of at most this many rows may take the fused int4 GEMM (fused_few_rows below).
+static constexpr int64_t kFewRows = 32;
+
 // The weight region holds the decoded int8 grid (row-major, or packed: n rounded up to 256 rows), or for the fused
-// few-row GEMM its split-K accumulators.
+// few-row GEMM its split-K accumulators (only calls that can take that GEMM reserve them).
 static size_t weight_region(int64_t m, int64_t n, int64_t k) {
   const size_t grid = static_cast<size_t>((n + 255) / 256 * 256) * k;
-  const size_t acc = static_cast<size_t>(h3k_gemm_w4a8_workspace(m, n, k));
+  const size_t acc = m <= kFewRows ? static_cast<size_t>(h3k_gemm_w4a8_workspace(m, n, k)) : 0;
   return grid > acc ? grid : acc;
 }
 
@@ -68,7 +71,7 @@ static bool packed_route(int64_t m, int64_t n, int64_t k, const void* q, int64_t
 // Chunks of up to 32 rows take the fused int4 GEMM; from 64 rows the decode + int8 GEMM pair is faster (N=13824,
 // K=5120: 35 against 42 us at 64 rows), at 16 the fused GEMM (15 against 34 us).
 static bool fused_few_rows(int64_t m, int64_t k, int group, const void* q, int64_t ldq) {
-  return m <= 32 && k % 64 == 0 && (group == 16 || group == 32 || (group > 0 && group % 64 == 0)) && k % group == 0 &&
+  return m <= kFewRows && k % 64 == 0 && (group == 16 || group == 32 || (group > 0 && group % 64 == 0)) && k % group == 0 &&
          aligned(q, 16) && ldq % 16 == 0;
 }
 

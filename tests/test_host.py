@@ -47,9 +47,12 @@ def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     assert lib.h3k_w4a8_linear(None, 0, 4, 256, 256, None, 128, None, 3, 16, None, None, 8, 16, 256, None, 0, None, 0, 8,
                                None, 0, None) == _lib.ESPACE
     # int8 activations + scales + the weight region: the decoded grid with n rounded up to 256 rows (the packed
-    # layout's padding), or the few-row GEMM's accumulators if larger
+    # layout's padding), or, for calls of at most 32 rows, the few-row GEMM's accumulators if larger
     assert lib.h3k_w4a8_linear_workspace(4, 8, 256) == 1024 + 256 + 256 * 256
     assert lib.h3k_w4a8_linear_workspace(600, 13824, 5120) == 600 * 5120 + 2560 + 13824 * 5120
+    # past the fused few-row GEMM's 32 rows no split-K accumulators are reserved: activations + scales + grid only
+    assert lib.h3k_w4a8_linear_workspace(4096, 13824, 5120) == 4096 * 5120 + 4096 * 4 + 13824 * 5120
+    assert lib.h3k_w4a8_linear_workspace(4096, 5120, 13824) <= 128 << 20  # fits the no-alloc entry's scratch
     # the packed grid's size and the shapes its GEMM serves
     assert lib.h3k_w8_packed_bytes(33, 128) == 256 * 128 and lib.h3k_w8_packed_bytes(32, 100) == -1
     assert lib.h3k_gemm_packed_serves(32768, 13824, 5120) == 1 and lib.h3k_gemm_packed_serves(512, 13824, 5120) == 0
