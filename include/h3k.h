@@ -152,6 +152,18 @@ int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * h3k_w4a8_linear without a workspace, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The scratch is a
+ * static device array of 128 MiB per GPU, held until the process ends; calls whose h3k_w4a8_linear_workspace(m, n, k)
+ * exceeds it fail with H3K_ESPACE (split the rows).  Nothing is allocated or freed.  Every call on a GPU uses that
+ * GPU's one array: calls that overlap on one GPU (two streams, two threads) race and must be ordered by the caller.
+ */
+int h3k_w4a8_linear_noalloc(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* q, int64_t ldq,
+                            const void* s_rel, int s_dtype, int64_t lds, const float* s_ch, const float* codebook,
+                            int64_t n, int group, int rot, const void* bias, int mode, void* out, int out_dtype,
+                            int64_t ldo, void* stream);
+
+/*
  * h3k_rotate_quant of an activation applied as the input is read, in one pass:
  *   act 1 (swiglu): x rows are [gate | up] (2k wide); the quantised input is silu(gate) * up, each op rounded to
  *                   the activation dtype -- replaces qlinear.py:376-379 (_swiglu) + :295-303 (quantize_activation)

@@ -34,6 +34,8 @@ SIGNATURES = {
     "h3k_gemm_w4a8": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _int, _i64, _ptr, _int, _ptr, _ptr, _i64, _i64, _i64,
                              _int, _ptr, _int, _i64, _ptr, _ptr, _ptr]),
     "h3k_w4a8_linear_workspace": (_size, [_i64, _i64, _i64]),
+    "h3k_w4a8_linear_noalloc": (_int, [_ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _int, _i64, _ptr, _ptr, _i64, _int,
+                                       _int, _ptr, _int, _ptr, _int, _i64, _ptr]),
     "h3k_w4a8_linear": (_int, [_ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _int, _i64, _ptr, _ptr, _i64, _int, _int,
                                _ptr, _int, _ptr, _int, _i64, _ptr, _size, _ptr]),
     "h3k_copy_h2d_async": (_int, [_ptr, _ptr, _size, _ptr]),
