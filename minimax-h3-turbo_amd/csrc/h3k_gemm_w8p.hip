@@ -26,8 +26,13 @@
 // the barrier: the DMA of stage kt + S into the stage just read; after the second half's MFMAs: the weight
 // fragments of step kt + S into the registers just consumed.  vmcnt retires in issue order, so the wait before a
 // step's barrier allows exactly the ops of the S - 2 newer steps (G each) -- plus, in the S - 1 steps after a
-// full-tile epilogue, its NEPI stores.  The epilogue stages each 32-row block of a wavefront's outputs through a
-// private LDS area and stores whole 128-byte lines, non-temporally.
+// full-tile epilogue, its NEPI stores.  Each tile's K loop is peeled into its first S steps, the steady steps and
+// its last S steps, so that the steady steps carry no branch at all (a taken branch stalls the wave's MFMA
+// stream while the instruction buffer refills); the first step's first MFMAs start from a zero accumulator, so
+// nothing clears the 256 accumulator registers between tiles.  The 16-bit epilogue stages each 32-row block of a
+// wavefront's raw accumulators through a private LDS area, reads 8 consecutive columns of a row per lane (their
+// scales and bias are fixed per lane for the whole tile) and stores whole 128-byte lines, non-temporally, with the
+// next tile's loads still in flight.
 #include "h3k_gemm_common.hpp"
 
 namespace h3k {
@@ -56,6 +61,13 @@ __device__ __forceinline__ u32x4 weight_rsrc(const void* p, uint32_t bytes) {
 // steps.  The assembly load is invisible to it, and the kernel's explicit waits cover it: the fragments of step kt
 // are part of the group whose arrival the wait before step kt - 1's barrier enforces.  Nothing but an MFMA reads
 // the destination registers, and none before that wait.
+// An fp32 value materialised as such (see fp32_round_point), as a plain asm statement rather than a volatile one:
+// it orders nothing else, so the scheduler stays free to overlap the epilogue's LDS reads with its arithmetic.
+__device__ __forceinline__ float value_point(float f) {
+  __asm__("" : "+v"(f));
+  return f;
+}
+
 template <int OFF>
 __device__ __forceinline__ void weight_load(v4i& dst, const u32x4& rsrc, uint32_t voff, uint32_t soff) {
   __asm__ volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:%4"
@@ -63,7 +75,14 @@ __device__ __forceinline__ void weight_load(v4i& dst, const u32x4& rsrc, uint32_
                    : "v"(voff), "s"(rsrc), "s"(soff), "n"(OFF));
 }
 
-template <int S, int ODT, bool EAGER, bool ACC>
+#ifndef H3K_W8P_EARLY
+#define H3K_W8P_EARLY 2
+#endif
+
+// Epilogue variants (a template parameter, so that no per-element branch splits the epilogue's code):
+enum { EPI_PLAIN16 = 0, EPI_BIAS16 = 1, EPI_GENERAL = 2, EPI_ACC = 3 };
+
+template <int S, int ODT, bool EAGER, int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restrict__ A, int64_t lda,
                                                           const int8_t* __restrict__ Bp, uint32_t bp_bytes, int NBP,
                                                           int M, int N, int K, const float* __restrict__ xs,
@@ -76,13 +95,20 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   constexpr int DPW = STAGE / 1024 / 4;  // 1 KiB direct-to-LDS loads per wavefront per stage
   constexpr int BPW = 2 * WNB;           // weight fragment loads per wavefront per step
   constexpr int G = DPW + BPW;           // vector-memory ops per wavefront per step
+  // EPI_PLAIN16 / EPI_BIAS16: 16-bit outputs without / with bias; EPI_GENERAL: fp32 outputs; EPI_ACC: any output
+  // with the accumulator dump (the last two handle bias at run time)
   constexpr bool STAGED = ODT != H3K_F32;
+  constexpr bool ACC = EPI == EPI_ACC;
+  constexpr bool FAST = EPI == EPI_PLAIN16 || EPI == EPI_BIAS16;
+  static_assert(!FAST || STAGED, "the 16-bit epilogue needs a 16-bit output");
   constexpr int NEPI = 8 * WMB;          // stores of one full-tile 16-bit epilogue per wavefront
   constexpr int GROW = 132;              // staging row pitch: 128 32-bit values + 4 of padding
   constexpr int RS = 2;                  // scale slots (tile t uses slot t % 2)
+  constexpr int SLOT = 768;              // floats per slot: 256 xs, 256 s_ch, then 1 KiB of bias
+  constexpr int BES = ODT == H3K_F32 ? 4 : 2;  // bias element bytes (the output dtype)
   constexpr int STEADY = G * (S - 2);
   static_assert(STEADY + NEPI + 1 < 64, "vmcnt allowance out of range");
-  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE + RS * 2048 + 4 * 32 * GROW * 4];
+  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE + RS * SLOT * 4 + 4 * 32 * GROW * 4];
   float* const sscale = reinterpret_cast<float*>(smem + S * STAGE);
 
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -127,11 +153,23 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     bnext = bfirst;
     astep = 0;
   };
-  auto load_scales = [&](int slot, int m0, int n0) {  // waves 0 and 1: the tile's 256 xs / 256 s_ch
-    if (wave < 2) {
-      const float* p = wave == 0 ? xs + (min(m0 + 4 * lane, M - 4) & ~3) : sch + min(n0 + 4 * lane, N - 4);
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(p), (lds_void*)(sscale + slot * 512 + wave * 256), 16,
-                                       0, 0);
+  // Waves 0, 1 and 2 load the tile's 256 xs, 256 s_ch and 256 bias values, one 16-byte chunk per lane.  A chunk
+  // past the end of its array is clamped to the 16-byte chunk that holds the last element (the arrays are 16-byte
+  // aligned, so that chunk lies in the same page as the element): the values it brings are those of rows or
+  // columns that are never stored.  Every stored row and column therefore reads its own value from the slot.
+  auto load_scales = [&](int slot, int m0, int n0) {
+    float* const dst = sscale + slot * SLOT + wave * 256;
+    if (wave == 0) {
+      const int r = min(m0 + 4 * lane, (M - 1) & ~3);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(xs + r), (lds_void*)dst, 16, 0, 0);
+    } else if (wave == 1) {
+      const int c = min(n0 + 4 * lane, (N - 1) & ~3);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(sch + c), (lds_void*)dst, 16, 0, 0);
+    } else if (EPI == EPI_BIAS16 && wave == 2 && lane * (16 / BES) < BN) {
+      constexpr int PER = 16 / BES;  // bias values per chunk
+      const int c = min(n0 + PER * lane, (N - 1) / PER * PER);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(static_cast<const char*>(bias) + c * BES),
+                                       (lds_void*)dst, 16, 0, 0);
     }
   };
   // Every step issues the same G vector-memory ops: after the last step of the last tile the loads re-read K
@@ -147,7 +185,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   };
   v4i bq[S][WNB][2];  // weight fragments of S steps
   auto issue_b = [&](auto u, bool real) {
-    const uint32_t b0 = real ? bnext : bfirst, b1 = b0 + 4096u;  // blocks 0-1 and 2-3: 12-bit immediate offsets
+    // values, not a conditional lvalue: a select between the two variables' addresses would keep both in memory
+    const uint32_t bn = bnext, bf = bfirst;
+    const uint32_t b0 = real ? bn : bf, b1 = b0 + 4096u;  // blocks 0-1 and 2-3: 12-bit immediate offsets
     weight_load<0>(bq[u][0][0], rb, bvoff, b0);
     weight_load<1024>(bq[u][0][1], rb, bvoff, b0);
     weight_load<2048>(bq[u][1][0], rb, bvoff, b0);
@@ -167,7 +207,6 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     static_for<WMB>([&](auto i) { af[i] = *reinterpret_cast<const v4i*>(base + swz(arow + i * 32, c)); });
   };
   v16i acc[WMB][WNB];
-  auto zero_acc = [&]() { static_for<WMB>([&](auto i) { static_for<WNB>([&](auto j) { acc[i][j] = v16i{}; }); }); };
   auto mfma = [&](const v4i (&af)[WMB], auto u, auto h) {
     static_for<WMB>([&](auto i) {
       static_for<WNB>([&](auto j) {
@@ -184,10 +223,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   auto scaled = [&](int a, float x, float s) -> float {
-    return fp32_round_point(EAGER ? static_cast<float>(a) * fp32_round_point(x * s)
-                                  : fp32_round_point(static_cast<float>(a) * x) * s);
+    return value_point(EAGER ? static_cast<float>(a) * value_point(x * s) : value_point(static_cast<float>(a) * x) * s);
   };
   auto bits16 = [&](float f) -> uint32_t { return ODT == H3K_F16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f); };
+  auto round16 = [&](float f) -> float { return ODT == H3K_F16 ? round_f16(f) : round_bf16(f); };
   auto pack4 = [&](const float (&f)[4]) -> uint2 {
     if (ODT == H3K_BF16) {
       const bf16x2 lo = __builtin_convertvector((f32x2){f[0], f[1]}, bf16x2);
@@ -197,68 +236,143 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     return make_uint2(bits16(f[0]) | (bits16(f[1]) << 16), bits16(f[2]) | (bits16(f[3]) << 16));
   };
 
-  // Stores the finished tile; true when exactly NEPI vector-memory ops were issued (the full-tile 16-bit path).
-  // One path computes every value: per 32-row block, the wavefront writes its fp32 results (and, if asked, the raw
-  // accumulators) into its staging area and reads them back row-contiguous.  Full tiles with 16-bit, line-aligned
-  // outputs then store 8 outputs per lane, whole 128-byte lines, non-temporally; everything else (tiles cut by M or
-  // N, bias, accumulator dump, fp32 or unaligned outputs) stores 4 per lane, predicated on M and N, after waiting for
-  // every load in flight -- the next tile's weight fragments included, so nothing in flight can be spilled there.
-  // A single path keeps the accumulator reads to one block at a time (two paths made the compiler read all 256
-  // ahead of the branch and spill).  The xs slot holds whole 16-byte chunks only where they lie inside [0, M), so a
-  // tile cut by M reads xs itself.
+  // Stores the finished tile; true when exactly NEPI vector-memory ops were issued (a whole 16-bit tile).
+  // Per 32-row block, the wavefront writes its accumulators into its staging area and reads them back
+  // row-contiguous, 8 columns per lane.
+  //   16-bit outputs: the raw int32 accumulators go through the staging area; the scale (and bias) of a lane's 8
+  //   columns are the same for every row, so they are read from the tile's slot once, and each row's xs is one
+  //   LDS read.  Rows inside M store 8 outputs as one 16-byte non-temporal store when the output rows are 16-byte
+  //   aligned and the 8 columns lie inside N, else element by element.  Nothing here waits for vector memory: the
+  //   next tile's loads stay in flight.
+  //   fp32 outputs or the accumulator dump: fp32 results (and the raw accumulators) are staged and stored 4 per
+  //   lane after waiting for every load in flight -- the next tile's weight fragments included, so nothing in
+  //   flight can be spilled there.
+  // One path per instantiation keeps the accumulator reads to one block at a time.
   auto epilogue = [&](int slot) -> bool {
     // lane- and tile-derived values recomputed from opaque copies: shared with the K loop's address arithmetic
     // they would stay live across it
     int lane = static_cast<int>(threadIdx.x & 63);
     __asm__ volatile("" : "+v"(lane));
     const int kh = lane >> 5;
-    const int row0 = cm0 + wm * 128 + (lane & 31);
-    const int col0 = cn0 + wn * 128 + kh * 4;
-    const float* const sx = sscale + slot * 512;
-    const bool full = cm0 + BM <= M && cn0 + BN <= N && vec_out && !ACC && bias == nullptr;
-    const bool lines = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (ldo & 7) == 0;
-    const bool fast = full && STAGED && lines;
-    if (!fast) {
-      __builtin_amdgcn_sched_barrier(0);
-      wait_vmcnt<0>();
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    float* const stg = reinterpret_cast<float*>(smem + S * STAGE + RS * 2048) + wave * (32 * GROW);
-    const bool cut_m = cm0 + BM > M;
-    static_for<WMB>([&](auto i) {
-      static_for<2>([&](auto pass) {  // 0: outputs, 1: accumulators (acc_out)
-        if (pass == 1 && !ACC) return;
+    const float* const sx = sscale + slot * SLOT;
+    float* const stg = reinterpret_cast<float*>(smem + S * STAGE + RS * SLOT * 4) + wave * (32 * GROW);
+    if constexpr (FAST) {
+      const int c8 = wn * 128 + (lane & 15) * 8;  // the lane's 8 columns, relative to the tile
+      const int gcol = cn0 + c8;
+      const bool lines = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (ldo & 7) == 0;
+      const bool cols_in = gcol + 8 <= N;
+      const bool whole = lines && cm0 + BM <= M && cn0 + BN <= N;  // every store a whole 16-byte vector
+      float sc[8], bv[8];
+      {
+        // element reads of the slot: a 16-byte LDS read of memory a direct-to-LDS load wrote makes the compiler
+        // wait for vmcnt(0), i.e. for the next tile's loads in flight
+        static_for<8>([&](auto e) { sc[e] = sx[256 + c8 + e]; });
+        if constexpr (EPI == EPI_BIAS16) {
+          const uint32_t* const b = reinterpret_cast<const uint32_t*>(sx + 512) + c8 / 2;  // 8 16-bit values
+          static_for<4>([&](auto e) {
+            const uint32_t two = b[e];
+            bv[2 * e] = ODT == H3K_F16 ? f16_to_f32(two & 0xFFFFu) : bf16_to_f32(two & 0xFFFFu);
+            bv[2 * e + 1] = ODT == H3K_F16 ? f16_to_f32(two >> 16) : bf16_to_f32(two >> 16);
+          });
+        }
+      }
+      static_for<WMB>([&](auto i) {
         __builtin_amdgcn_sched_barrier(0);
-        const float x = cut_m ? xs[min(row0 + i * 32, M - 1)] : sx[row0 - cm0 + i * 32];
-        float* const w = stg + (lane & 31) * GROW + kh * 4;
+        int32_t* const w = reinterpret_cast<int32_t*>(stg) + (lane & 31) * GROW + kh * 4;
         static_for<WNB>([&](auto j) {
           static_for<4>([&](auto g) {
-            // element reads of the scale slot: a 16-byte LDS read here makes the compiler drain vmcnt
-            const float* p = sx + 256 + col0 - cn0 + j * 32 + g * 8;
-            float4 v;
-            if (pass == 0) {
-              v = make_float4(scaled(acc[i][j][g * 4 + 0], x, p[0]), scaled(acc[i][j][g * 4 + 1], x, p[1]),
-                              scaled(acc[i][j][g * 4 + 2], x, p[2]), scaled(acc[i][j][g * 4 + 3], x, p[3]));
-            } else {
-              v = make_float4(__int_as_float(acc[i][j][g * 4 + 0]), __int_as_float(acc[i][j][g * 4 + 1]),
-                              __int_as_float(acc[i][j][g * 4 + 2]), __int_as_float(acc[i][j][g * 4 + 3]));
-            }
-            *reinterpret_cast<float4*>(w + j * 32 + g * 8) = v;
+            *reinterpret_cast<v4i*>(w + j * 32 + g * 8) =
+                v4i{acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]};
           });
         });
         wave_lds_sync();
-        if (fast) {
-          static_for<8>([&](auto q) {  // 4 rows x 256 bytes per store instruction
-            const int rr = q * 4 + (lane >> 4);
-            const float* rp = stg + rr * GROW + (lane & 15) * 8;
-            const float4 lo = *reinterpret_cast<const float4*>(rp), hi = *reinterpret_cast<const float4*>(rp + 4);
-            const uint2 a = pack4({lo.x, lo.y, lo.z, lo.w}), b = pack4({hi.x, hi.y, hi.z, hi.w});
-            u32x4* dst = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) +
-                                                  static_cast<int64_t>(cm0 + wm * 128 + i * 32 + rr) * ldo + cn0 +
-                                                  wn * 128 + (lane & 15) * 8);
-            __builtin_nontemporal_store(u32x4{a.x, a.y, b.x, b.y}, dst);
+        const float* const xr = sx + wm * 128 + i * 32 + (lane >> 4);
+        // the 8 outputs of row q * 4 + (lane >> 4) of the block at the lane's 8 columns, from its raw accumulators
+        auto row_out = [&](const v4i& lo, const v4i& hi, float x, float (&f)[8]) {
+          const int a[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          static_for<8>([&](auto e) {
+            float y = scaled(a[e], x, sc[e]);
+            if constexpr (EPI == EPI_BIAS16)  // added after the output rounding (qlinear.py:404-405)
+              y = value_point(round16(y) + bv[e]);
+            f[e] = y;
+          });
+        };
+        const int32_t* const rp = reinterpret_cast<const int32_t*>(stg) + (lane >> 4) * GROW + (lane & 15) * 8;
+        const int row_b = cm0 + wm * 128 + i * 32 + (lane >> 4);  // the lane's row for q = 0
+        uint16_t* const obase = static_cast<uint16_t*>(out) + static_cast<int64_t>(row_b) * ldo + gcol;
+        if (whole) {
+          // the accumulators of RB rows read first (8 RB registers): the LDS latency is paid once per batch, and
+          // no branch splits the arithmetic and the stores.  With bias, whose 8 values take registers too, batches
+          // of 4 rows keep the epilogue from spilling the next tile's weight registers.
+          constexpr int RB = EPI == EPI_BIAS16 ? 4 : 8;
+          static_for<8 / RB>([&](auto bt) {
+            v4i lo[RB], hi[RB];
+            float x[RB];
+            static_for<RB>([&](auto r) {
+              constexpr int q = decltype(bt)::value * RB + decltype(r)::value;
+              lo[r] = *reinterpret_cast<const v4i*>(rp + q * 4 * GROW);
+              hi[r] = *reinterpret_cast<const v4i*>(rp + q * 4 * GROW + 4);
+              x[r] = xr[q * 4];
+            });
+            static_for<RB>([&](auto r) {
+              constexpr int q = decltype(bt)::value * RB + decltype(r)::value;
+              float f[8];
+              row_out(lo[r], hi[r], x[r], f);
+              const uint2 p0 = pack4({f[0], f[1], f[2], f[3]}), p1 = pack4({f[4], f[5], f[6], f[7]});
+              __builtin_nontemporal_store(u32x4{p0.x, p0.y, p1.x, p1.y},
+                                          reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(q * 4) * ldo));
+            });
           });
         } else {
+          static_for<8>([&](auto q) {
+            const v4i lo = *reinterpret_cast<const v4i*>(rp + q * 4 * GROW);
+            const v4i hi = *reinterpret_cast<const v4i*>(rp + q * 4 * GROW + 4);
+            float f[8];
+            row_out(lo, hi, xr[q * 4], f);
+            if (row_b + q * 4 < M) {
+              uint16_t* const orow = obase + static_cast<int64_t>(q * 4) * ldo;
+              if (lines && cols_in) {
+                const uint2 p0 = pack4({f[0], f[1], f[2], f[3]}), p1 = pack4({f[4], f[5], f[6], f[7]});
+                *reinterpret_cast<u32x4*>(orow) = u32x4{p0.x, p0.y, p1.x, p1.y};
+              } else {
+                static_for<8>([&](auto e) {
+                  if (gcol + e < N) orow[e] = static_cast<uint16_t>(bits16(f[e]));
+                });
+              }
+            }
+          });
+        }
+        wave_lds_sync();  // the next block overwrites the staging area
+      });
+      return whole;
+    } else {
+      const int row0 = cm0 + wm * 128 + (lane & 31);
+      const int col0 = cn0 + wn * 128 + kh * 4;
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<0>();
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<WMB>([&](auto i) {
+        static_for<2>([&](auto pass) {  // 0: outputs, 1: accumulators (acc_out)
+          if (pass == 1 && !ACC) return;
+          __builtin_amdgcn_sched_barrier(0);
+          const float x = sx[row0 - cm0 + i * 32];
+          float* const w = stg + (lane & 31) * GROW + kh * 4;
+          static_for<WNB>([&](auto j) {
+            static_for<4>([&](auto g) {
+              // element reads of the scale slot: a 16-byte LDS read here makes the compiler drain vmcnt
+              const float* p = sx + 256 + col0 - cn0 + j * 32 + g * 8;
+              float4 v;
+              if (pass == 0) {
+                v = make_float4(scaled(acc[i][j][g * 4 + 0], x, p[0]), scaled(acc[i][j][g * 4 + 1], x, p[1]),
+                                scaled(acc[i][j][g * 4 + 2], x, p[2]), scaled(acc[i][j][g * 4 + 3], x, p[3]));
+              } else {
+                v = make_float4(__int_as_float(acc[i][j][g * 4 + 0]), __int_as_float(acc[i][j][g * 4 + 1]),
+                                __int_as_float(acc[i][j][g * 4 + 2]), __int_as_float(acc[i][j][g * 4 + 3]));
+              }
+              *reinterpret_cast<float4*>(w + j * 32 + g * 8) = v;
+            });
+          });
+          wave_lds_sync();
           const int r2 = lane >> 5, c4 = (lane & 31) * 4;  // rows r2 + 2q, columns c4 .. c4 + 3 of the block
           const int n = cn0 + wn * 128 + c4;
           static_for<16>([&](auto q) {
@@ -275,7 +389,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
                 float o[4];
                 static_for<4>([&](auto e) {
                   float y = f[e];
-                  if (ODT != H3K_F32) y = ODT == H3K_F16 ? round_f16(y) : round_bf16(y);
+                  if (ODT != H3K_F32) y = round16(y);
                   if (bias && n + e < N) {  // added after the output rounding (qlinear.py:404-405)
                     float b;
                     if (ODT == H3K_F32) b = static_cast<const float*>(bias)[n + e];
@@ -303,12 +417,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
               }
             }
           });
-        }
-        wave_lds_sync();  // the next block overwrites the staging area
+          wave_lds_sync();  // the next block overwrites the staging area
+        });
       });
-    });
-    if (!fast) wait_vmcnt<0>();  // nothing of unknown count stays pending into the next tile's first steps
-    return fast;
+      wait_vmcnt<0>();  // nothing of unknown count stays pending into the next tile's first steps
+      return false;
+    }
   };
 
   // ---------------------------------------------------------------- prologue
@@ -321,48 +435,97 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   });
   wait_vmcnt<G * (S - 1)>();
   lds_barrier();
-  zero_acc();
 
   v4i a0[WMB], a1[WMB];
   read_frags(0, 0, a0);
   bool exact = false;  // the last epilogue issued exactly NEPI vector-memory ops
-  for (int it = 0; it < T; ++it) {
-    const bool has_next = it + 1 < T;
+  bool has_next = false;
+  int it = 0;
+
+  // One K-step in stage u.  FIRST: the tile's first step, whose first MFMAs start from zero (no accumulator
+  // clearing between tiles).  WAIT: which allowance the wait before the barrier uses -- step kt + 1 must have
+  // landed; normally the S - 2 newer steps may still be in flight (W_STEADY); in the S - 1 steps after an epilogue
+  // its stores (and the scale loads) sit in between (W_AFTER_EPI); in the last tile's last steps wait for everything
+  // (W_TAIL), or for everything without issuing loads (W_DRAIN: the last steps of a tile whose epilogue does not
+  // run across the next tile's loads).  more: step kt + S exists (this tile's or the next one's); frags: step
+  // kt + 1 is this tile's.  The steady steps have every choice fixed at compile time: no branch interrupts their
+  // MFMA stream.
+  enum { W_STEADY = 0, W_AFTER_EPI = 1, W_TAIL = 2, W_DRAIN = 3 };
+  auto step = [&](auto u, auto first, auto wait, bool more, bool frags) {
+    read_frags(u, 1, a1);
+    if constexpr (first.value) {
+      static_for<WMB>([&](auto i) {
+        static_for<WNB>([&](auto j) { acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bq[u][j][0], a0[i], v16i{}, 0, 0, 0); });
+      });
+    } else {
+      mfma(a0, u, std::integral_constant<int, 0>{});
+    }
+    // the second half's fragment reads go out behind the first MFMAs rather than at the end of the group: their
+    // latency then hides under the remaining MFMAs instead of stalling the wait before the barrier
+    __builtin_amdgcn_sched_group_barrier(0x008, H3K_W8P_EARLY, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);                 // LDS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 16 - H3K_W8P_EARLY, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkmcnt0();
+    if constexpr (wait.value == W_STEADY) {
+      wait_vmcnt<STEADY>();
+    } else if constexpr (wait.value == W_AFTER_EPI) {
+      if (it == 0) wait_vmcnt<STEADY>();
+      else if (exact) wait_vmcnt<STEADY + NEPI>();
+      else wait_vmcnt<0>();
+    } else if constexpr (wait.value == W_TAIL) {
+      if (has_next) wait_vmcnt<STEADY>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
+    if constexpr (wait.value != W_DRAIN) issue_a(u, more);  // stage kt + S into the stage just read
+    if (frags) read_frags((u + 1) % S, 0, a0);
+    mfma(a1, u, std::integral_constant<int, 1>{});
+    if constexpr (wait.value != W_DRAIN) issue_b(u, more);  // weight fragments of step kt + S into the registers just consumed
+  };
+  // The 16-bit epilogue runs with the next tile's first S steps of loads in flight.  The fp32 and accumulator-dump
+  // epilogues need more registers than that leaves: their tiles end with the load streams drained and start the
+  // next tile's streams afresh, as the prologue does.
+  constexpr bool CROSS = FAST;
+  using std::integral_constant;
+  for (; it < T; ++it) {
+    has_next = it + 1 < T;
     int nm0 = 0, nn0 = 0;  // the next tile's origin
     if (has_next) coords(it + 1, nm0, nn0);
-    if (it > 0) load_scales(it % RS, cm0, cn0);
-    for (int kt0 = 0; kt0 < KT; kt0 += S) {
-      static_for<S>([&](auto u) {
-        const int kt = kt0 + u;
-        const bool last = kt == KT - 1;
-        const bool more = has_next || kt < KT - S;  // step kt + S exists (this tile's or the next one's)
-        if (kt == KT - S && has_next) point_loads(nm0, nn0);  // the load streams move on to the next tile
-        read_frags(u, 1, a1);
-        mfma(a0, u, std::integral_constant<int, 0>{});
-        __builtin_amdgcn_sched_barrier(0);
-        wait_lgkmcnt0();
-        // step kt + 1 must have landed: normally S - 2 newer steps may still be in flight; in the S - 1 steps after
-        // an epilogue its stores (and waves 0-1's scale load) sit in between; in the last tile's last steps wait for
-        // everything
-        if (it > 0 && kt < S - 1) {
-          if (exact) wait_vmcnt<STEADY + NEPI>();
-          else wait_vmcnt<0>();
-        } else if (!has_next && kt >= KT - S) {
-          wait_vmcnt<0>();
-        } else {
-          wait_vmcnt<STEADY>();
-        }
+    if (it > 0) {
+      if constexpr (CROSS) {
+        load_scales(it % RS, cm0, cn0);
+      } else {
+        point_loads(cm0, cn0);
+        load_scales(it % RS, cm0, cn0);
+        static_for<S>([&](auto s) {
+          issue_a(s, true);
+          issue_b(s, true);
+        });
+        wait_vmcnt<G * (S - 1)>();
         lds_barrier();
-        issue_a(u, more);  // stage kt + S into the stage just read
-        if (!last) read_frags((u + 1) % S, 0, a0);
-        mfma(a1, u, std::integral_constant<int, 1>{});
-        issue_b(u, more);  // weight fragments of step kt + S into the registers just consumed
+        read_frags(0, 0, a0);
+      }
+    }
+    static_for<S>([&](auto u) {  // steps 0 .. S - 1 (K has at least 2 S steps)
+      constexpr int U = decltype(u)::value;
+      step(u, integral_constant<bool, U == 0>{}, integral_constant<int, U < S - 1 ? W_AFTER_EPI : W_STEADY>{}, true, true);
+    });
+    for (int kt0 = S; kt0 < KT - S; kt0 += S) {
+      static_for<S>([&](auto u) {
+        step(u, integral_constant<bool, false>{}, integral_constant<int, W_STEADY>{}, true, true);
       });
     }
+    if (CROSS && has_next) point_loads(nm0, nn0);  // the load streams move on to the next tile
+    static_for<S>([&](auto u) {  // steps KT - S .. KT - 1
+      step(u, integral_constant<bool, false>{}, integral_constant<int, CROSS ? W_TAIL : W_DRAIN>{}, has_next,
+           decltype(u)::value < S - 1);
+    });
     exact = epilogue(it % RS);
-    zero_acc();
     if (has_next) {
-      read_frags(0, 0, a0);
+      if constexpr (CROSS) read_frags(0, 0, a0);
       cm0 = nm0;
       cn0 = nn0;
     }
@@ -374,13 +537,13 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
 #define H3K_W8P_S 4
 #endif
 
-template <int ODT, bool EAGER, bool ACC>
+template <int ODT, bool EAGER, int EPI>
 static void launch(const int8_t* a, int64_t lda, const int8_t* bp, uint32_t bp_bytes, int nbp, int m, int n, int k,
                    const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, int grid,
                    hipStream_t st) {
   const size_t es = ODT == H3K_F32 ? 4 : 2;
   const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
-  hipLaunchKernelGGL((gemm_w8p_kernel<H3K_W8P_S, ODT, EAGER, ACC>), dim3(grid), dim3(256), 0, st, a, lda, bp, bp_bytes,
+  hipLaunchKernelGGL((gemm_w8p_kernel<H3K_W8P_S, ODT, EAGER, EPI>), dim3(grid), dim3(256), 0, st, a, lda, bp, bp_bytes,
                      nbp, m, n, k, xs, sch, bias, out, ldo, acc, vec_out);
 }
 
@@ -433,15 +596,16 @@ void gemm_w8p_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
   const uint32_t bytes = static_cast<uint32_t>(w8p_bytes(n, k));
   const int nbp = static_cast<int>((n + 255) / 256 * 8);
   const bool e = mode == H3K_MODE_EAGER;
-#define H3K_L(D, E, C) w8p::launch<D, E, C>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid, st)
-  if (acc_out) {  // the accumulator dump: its own instantiations (a second read of every accumulator costs registers)
-    if (odt == H3K_BF16) { if (e) H3K_L(H3K_BF16, true, true); else H3K_L(H3K_BF16, false, true); }
-    else if (odt == H3K_F16) { if (e) H3K_L(H3K_F16, true, true); else H3K_L(H3K_F16, false, true); }
-    else { if (e) H3K_L(H3K_F32, true, true); else H3K_L(H3K_F32, false, true); }
+#define H3K_L(D, P)                                                                                              \
+  (e ? w8p::launch<D, true, P>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid, st)     \
+     : w8p::launch<D, false, P>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid, st))
+  // the accumulator dump has its own instantiations (a second read of every accumulator costs registers)
+  if (odt == H3K_F32) {
+    if (acc_out) H3K_L(H3K_F32, w8p::EPI_ACC); else H3K_L(H3K_F32, w8p::EPI_GENERAL);
+  } else if (odt == H3K_F16) {
+    if (acc_out) H3K_L(H3K_F16, w8p::EPI_ACC); else if (bias) H3K_L(H3K_F16, w8p::EPI_BIAS16); else H3K_L(H3K_F16, w8p::EPI_PLAIN16);
   } else {
-    if (odt == H3K_BF16) { if (e) H3K_L(H3K_BF16, true, false); else H3K_L(H3K_BF16, false, false); }
-    else if (odt == H3K_F16) { if (e) H3K_L(H3K_F16, true, false); else H3K_L(H3K_F16, false, false); }
-    else { if (e) H3K_L(H3K_F32, true, false); else H3K_L(H3K_F32, false, false); }
+    if (acc_out) H3K_L(H3K_BF16, w8p::EPI_ACC); else if (bias) H3K_L(H3K_BF16, w8p::EPI_BIAS16); else H3K_L(H3K_BF16, w8p::EPI_PLAIN16);
   }
 #undef H3K_L
 }

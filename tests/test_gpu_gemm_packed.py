@@ -138,9 +138,11 @@ def test_packed_gemm_matches_int_mm_and_the_rowmajor_gemm(m, n, k):
 
 @pytest.mark.parametrize("mode", ["ck", "eager"])
 @pytest.mark.parametrize("odt", [_lib.BF16, _lib.F16, _lib.F32])
-def test_packed_gemm_epilogues_bias_and_strided_outputs(mode, odt):
-    m, n, k = 2000, 5120, 512
-    print(f"packed epilogue mode={mode} odt={odt}", flush=True)
+@pytest.mark.parametrize("m,n,k", [(2000, 5120, 512), (4090, 7000, 512)], ids=["cut_m", "cut_m_n_odd_rows"])
+def test_packed_gemm_epilogues_bias_and_strided_outputs(mode, odt, m, n, k):
+    # whole tiles and tiles cut by M (and N); M % 4 != 0 puts the last xs chunk across the end of xs; ldo = n + 4
+    # leaves 16-bit output rows 8-byte aligned only (element stores)
+    print(f"packed epilogue mode={mode} odt={odt} m={m} n={n} k={k}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(odt * 3 + (mode == "eager"))
     xq = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8, device=DEV)
     w8 = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8, device=DEV)
@@ -151,7 +153,7 @@ def test_packed_gemm_epilogues_bias_and_strided_outputs(mode, odt):
     w8p = pack(w8)
     acc = torch._int_mm(xq, w8.t())
     for b in (None, bias):
-        for ldo in (n, n + 8):
+        for ldo in (n, n + 8, n + 4):
             got, _ = run_packed(xq, xs, w8p, s_ch, n, mode, odt, bias=b, ldo=ldo)
             want = torch_epilogue(acc, xs, s_ch, mode, dt, b)
             assert torch.equal(got.contiguous().view(torch.uint8), want.view(torch.uint8)), (b is not None, ldo)
