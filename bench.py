@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--no-block", action="store_true", help="skip the config-4 DiT block measurement")
     ap.add_argument("--block-steps", type=int, default=5)
     ap.add_argument("--no-stream", action="store_true", help="skip the config-5 streamed 60-block stack")
-    ap.add_argument("--sweep", action="store_true", help="add the config-3 GEMM sweep (16 shapes) to the line")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the config-3 GEMM sweep (16 shapes)")
     ap.add_argument("--stream-blocks", type=int, default=60)
     ap.add_argument("--no-h3t", action="store_true", help="skip the .h3t container measurement")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model forward at the H3 shape")
@@ -424,24 +424,32 @@ def sweep_measurement(dev, steps: int):
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     rows = []
     for k, n in ((5120, 5120), (5120, 15360), (5120, 13824), (13824, 5120)):
         q, s_rel, s_ch, cb = synth_weight(n, k, dev)
         dw = ql._DevWeight(W4A8Weight(q, s_rel, s_ch, cb, group_size=128, convrot=256))
-        w8 = torch.empty(n, k, dtype=torch.int8, device=dev)
+        w8 = torch.empty(lib.h3k_w8_packed_bytes(n, k), dtype=torch.int8, device=dev)  # >= n * k
         for m in (512, 4096, 12090, 32768):
             g = torch.Generator(device=dev).manual_seed(m)
             x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
             xq = torch.empty(m, k, dtype=torch.int8, device=dev)
             xs = torch.empty(m, 1, dtype=torch.float32, device=dev)
             out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-            calls = [
-                lambda: lib.h3k_rotate_quant(x.data_ptr(), _lib.BF16, m, k, k, 256, 0, xq.data_ptr(), k, xs.data_ptr(), sp),
-                lambda: lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(), n, k,
-                                          128, w8.data_ptr(), k, sp),
-                lambda: lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, dw.s_ch.data_ptr(), None, m, n,
-                                          k, 0, out.data_ptr(), _lib.BF16, n, None, sp),
-            ]
+            packed = bool(lib.h3k_gemm_packed_serves(m, n, k))  # the route qlinear.linear takes
+            rq = lambda: lib.h3k_rotate_quant(x.data_ptr(), _lib.BF16, m, k, k, 256, 0, xq.data_ptr(), k, xs.data_ptr(), sp)
+            if packed:
+                calls = [rq,
+                         lambda: lib.h3k_decode_w4_packed(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds,
+                                                          dw.cb.data_ptr(), n, k, 128, w8.data_ptr(), sp),
+                         lambda: lib.h3k_gemm_a8w8_packed(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), dw.s_ch.data_ptr(),
+                                                          None, m, n, k, 0, out.data_ptr(), _lib.BF16, n, None, sp)]
+            else:
+                calls = [rq,
+                         lambda: lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(),
+                                                   n, k, 128, w8.data_ptr(), k, sp),
+                         lambda: lib.h3k_gemm_a8w8(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), k, dw.s_ch.data_ptr(), None,
+                                                   m, n, k, 0, out.data_ptr(), _lib.BF16, n, None, sp)]
             for _ in range(2):
                 for c in calls:
                     _lib.check(c(), "sweep")
@@ -456,13 +464,52 @@ def sweep_measurement(dev, steps: int):
             torch.cuda.synchronize()
             t = [sum(a.elapsed_time(b) for a, b in e) / len(e) for e in ev]
             ops = 2.0 * m * n * k
-            rows.append({"m": m, "k": k, "n": n, "rotquant_ms": round(t[0], 4), "decode_ms": round(t[1], 4),
+            rows.append({"m": m, "k": k, "n": n, "kernel": gemm_kernel_name(m, n, k, packed, cus),
+                         "rotquant_ms": round(t[0], 4), "decode_ms": round(t[1], 4),
                          "gemm_ms": round(t[2], 4), "gemm_TOPS": round(ops / (t[2] * 1e-3) / 1e12, 1),
                          "op_TOPS": round(ops / (sum(t) * 1e-3) / 1e12, 1),
                          "gemm_frac_peak": round(ops / (t[2] * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)})
             del x, xq, xs, out
         del dw, w8
     return rows
+
+
+def rotquant_config2(dev, steps: int = 20, rot: int = 256):
+    """rotate + quantise bf16 activations [12090, 5120] (1 % outlier channels x20), per-token
+    int8 output and fp32 scales; mean of `steps` launches (HIP events on the launch stream), HBM bytes = 2 MK
+    read + MK + 4 M written."""
+    import torch
+
+    from h3turbo_amd import _lib
+
+    lib = _lib.load()
+    m, k = 12090, 5120
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn(m, k, generator=g, device=dev)
+    x[:, torch.randperm(k, generator=g, device=dev)[: round(0.01 * k)]] *= 20
+    x = x.to(torch.bfloat16)
+    xq = torch.empty(m, k, dtype=torch.int8, device=dev)
+    xs = torch.empty(m, 1, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    def call():
+        _lib.check(lib.h3k_rotate_quant(x.data_ptr(), _lib.BF16, m, k, k, rot, 0, xq.data_ptr(), k, xs.data_ptr(), sp), "rq2")
+
+    for _ in range(3):
+        call()
+    ev = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        call()
+        e1.record(stream)
+        ev.append((e0, e1))
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    nbytes = 2 * m * k + m * k + 4 * m
+    return {"m": m, "k": k, "rot": rot, "ms": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
 def few_rows_measurement(dev, steps: int):
@@ -570,7 +617,37 @@ def cpu_baseline(m: int, k: int, n: int, rows: int):
     return {"value": round(2.0 * m * n * k / total / 1e12, 4), "unit": "TOPS", "cores": int(threads), "kind": "port",
             "sample": f"oracle/qlinear_ref.py on {rows} of {m} rows (K={k}, N={n}) + one per-call weight decode, "
                       f"median of 3; scaled to {m} rows: decode {td:.2f} s + rows {tr:.2f} s x {m / rows:.0f}",
-            "seconds_for_full_op": round(total, 2)}
+            "seconds_for_full_op": round(total, 2), "config1": cpu_config1(threads)}
+
+
+def cpu_config1(threads: int, runs: int = 7):
+    """BASELINE config 1 measured whole on the host: one W4A8 ConvRot QLinear, bf16 activations [256, 1024] with 1 %
+    outlier channels x20, int4 group-128 weight with fp16 scales [1024, 1024], seed 0, through the CPU oracle (weight
+    decode + rotate/quantise + exact int8 GEMM + epilogue); one warm-up, then the median of `runs` runs.  Rotation
+    256: the reference rejects the config's 128 (its Hadamard sizes are powers of 4)."""
+    import numpy as np
+
+    import inputs as gi
+    from oracle import qlinear_ref as ref
+
+    m, k, n = 256, 1024, 1024
+    x = ref.bf16_from_bits(gi.activations(m, k, seed=0))
+    q, s_rel, s_ch, cb = gi.weight_int4_g128(n, k, seed=0)
+
+    def once():
+        w8 = ref.decode_int8_grid(q, s_rel, "f16", cb, 128)
+        xq, xs = ref.quantize_rows(x, "bf16", 256, "ck")
+        return ref.epilogue(ref.int8_mm_emulated(xq, w8), xs, s_ch, "bf16", "ck")
+
+    once()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"ms": round(med * 1e3, 2), "TOPS": round(2.0 * m * n * k / med / 1e12, 6), "cores": int(threads),
+            "runs": runs, "sample": f"config 1 whole: M={m} K={k} N={n}, rotation 256, median of {runs} after 1 warm-up"}
 
 
 def main() -> None:
@@ -690,10 +767,11 @@ def main() -> None:
             "gemm_a8w8": {"ms": round(t_gemm, 4), "TOPS": round(gemm_tops, 1)},
         },
     }
+    line["kernels"]["rotate_quant_config2"] = rotquant_config2(dev)
     if not args.no_block:
         del xq, w8, out
         line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))
-    if args.sweep:
+    if not args.no_sweep:
         line["sweep"] = sweep_measurement(dev, 10)
     if not args.no_few_rows:
         line["few_rows"] = few_rows_measurement(dev, 20)
