@@ -1,19 +1,25 @@
-""".h3t: the block-contiguous safetensors container the weight-streaming engine reads (h3turbo/h3/store.py,
-h3turbo/h3/writer.py).
+""".h3t: the block-contiguous safetensors container of the H3 DiT weights (format of h3turbo/h3/store.py:1-40 and
+h3turbo/h3/writer.py:137-262; files written here are byte-identical to the reference writer's for the same tensors).
 
-An .h3t file is a valid safetensors file whose tensors are ordered globals first, then block 0 .. N-1.  Every
-block is one BLOCK_ALIGN-aligned byte range with the same tensor layout in every block, every tensor starts on a
-TENSOR_ALIGN boundary, and the gaps are explicit `__pad.<i>` U8 tensors (safetensors has no holes).  The
-metadata carries the format tag, the H3Config JSON, the block size / start / ranges and the block layout.  This
-module writes byte-identical files to the reference writer for the same tensors and reads the reference's files.
+The format, as this module implements it:
+  * a safetensors file: an 8-byte little-endian header length, a compact JSON header ("__metadata__" first, then
+    one entry per tensor in file order), then the data section;
+  * the JSON is padded with spaces so the data section starts on a BLOCK_ALIGN (4 KiB) boundary;
+  * the data section holds the globals (patch/condition projections, final layer, token refiner), then block
+    0 .. N-1; every tensor starts on a TENSOR_ALIGN (256 B) boundary, every block is one BLOCK_ALIGN-aligned range
+    of the same size with the same relative layout; gaps are explicit "__pad.<i>" U8 tensors, since safetensors
+    has no holes;
+  * tensors are placed in a canonical order (below), which fixes every offset;
+  * the metadata carries the format tag and version, the H3Config JSON, the block size / start / ranges, the block
+    and globals layouts and the quantisation parameters.
 
-On MI355X the reader is the host side of the streaming engine: `H3TFile` maps the file read-only and hands out
-zero-copy views (`block_tensor(i)`, a block's raw bytes; `block_weights_from(buf)`, typed views of a block held in
-any buffer, e.g. an HBM slot).  `blockstore.HostBlockStore.from_h3t` copies the blocks into pinned host memory,
-so each block then reaches HBM as one DMA transfer.
+Why the layout matters on MI355X: a block is one contiguous range, so it reaches HBM as ONE DMA transfer (from a
+pinned copy, `blockstore.HostBlockStore.from_h3t`), and the kernels read its tensors as typed views of the HBM
+slot (`H3TFile.block_weights_from`), 256-byte aligned for the 16-byte vector loads.
 """
 from __future__ import annotations
 
+import dataclasses
 import json
 import math
 import mmap
@@ -22,11 +28,13 @@ import re
 import struct
 import sys
 import warnings
+from dataclasses import dataclass
 from typing import Callable, Dict, Iterable, Iterator, List, Mapping, NamedTuple, Optional, Sequence, Tuple, Union
 
 import numpy as np
 import torch
 
+from .blockstore import BlockLayout, LayoutEntry
 from .config import H3Config
 from .types import BlockWeights, GlobalWeights, W4A8Weight, Weight
 
@@ -38,67 +46,187 @@ VERSION = 1
 TENSOR_ALIGN = 256
 BLOCK_ALIGN = 4096
 PAD_PREFIX = "__pad."
-_HEADER_CAP = 100_000_000
+_MAX_HEADER = 100_000_000  # a larger header is taken as garbage, not parsed
 
-# safetensors dtype name -> (torch dtype, bytes per element)
-_DT: Dict[str, Tuple[torch.dtype, int]] = {
-    "F64": (torch.float64, 8), "F32": (torch.float32, 4), "F16": (torch.float16, 2), "BF16": (torch.bfloat16, 2),
-    "I64": (torch.int64, 8), "I32": (torch.int32, 4), "I16": (torch.int16, 2), "I8": (torch.int8, 1),
-    "U8": (torch.uint8, 1), "BOOL": (torch.bool, 1), "F8_E4M3": (torch.float8_e4m3fn, 1),
-    "F8_E5M2": (torch.float8_e5m2, 1),
-}
-_NAME_OF = {t: name for name, (t, _) in _DT.items()}
+_TORCH = {"F64": torch.float64, "F32": torch.float32, "F16": torch.float16, "BF16": torch.bfloat16,
+          "I64": torch.int64, "I32": torch.int32, "I16": torch.int16, "I8": torch.int8, "U8": torch.uint8,
+          "BOOL": torch.bool, "F8_E4M3": torch.float8_e4m3fn, "F8_E5M2": torch.float8_e5m2}
+_ST_NAME = {t: n for n, t in _TORCH.items()}
 
-# The W4A8 linears of a block and the tensors each one carries (the checkpoint's naming).
 LINEARS = ("attn.qkv_proj", "attn.out_proj", "mlp.fc1", "mlp.fc2")
 QUANT_PARTS = ("weight", "weight_s_rel", "weight_s_channel", "weight_codebook", "comfy_quant")
-# Canonical tensor order inside a block and among the globals; anything else follows sorted by name.  The order
-# decides every offset, so it is part of the format (the reference writer uses the same order).
-BLOCK_ORDER = ("adaln_proj.linear.weight", "adaln_proj.linear.bias", "norm1.weight", "attn.q_norm.weight",
-               "attn.k_norm.weight", *(f"attn.qkv_proj.{p}" for p in QUANT_PARTS),
-               *(f"attn.out_proj.{p}" for p in QUANT_PARTS), "norm2.weight", *(f"mlp.fc1.{p}" for p in QUANT_PARTS),
-               *(f"mlp.fc2.{p}" for p in QUANT_PARTS))
-GLOBAL_ORDER = ("video_patch_proj.weight", "video_patch_proj.bias", "audio_patch_proj.weight", "audio_patch_proj.bias",
-                "condition_proj.weight", "condition_proj.bias", "adaln_t_table", "rope.inv_freq",
-                "final_layer.norm.weight", "final_layer.adaln_proj.linear.weight", "final_layer.adaln_proj.linear.bias",
-                "final_layer.video_out.weight", "final_layer.video_out.bias", "final_layer.audio_out.weight",
-                "final_layer.audio_out.bias")
-_BLOCK_NAME = re.compile(r"^blocks\.(\d+)\.(.+)$")
-_REFINER_NAME = re.compile(r"^token_refiner\.blocks\.(\d+)\.(.+)$")
 
 
 class H3TError(ValueError):
     """Not a valid .h3t container, or an inconsistent write request."""
 
 
-def itemsize(dtype: str) -> int:
-    if dtype not in _DT:
-        raise H3TError(f"unsupported safetensors dtype {dtype!r}")
-    return _DT[dtype][1]
-
-
 def torch_dtype(dtype: str) -> torch.dtype:
-    itemsize(dtype)
-    return _DT[dtype][0]
+    try:
+        return _TORCH[dtype]
+    except KeyError:
+        raise H3TError(f"unsupported safetensors dtype {dtype!r}") from None
+
+
+def itemsize(dtype: str) -> int:
+    return torch.empty((), dtype=torch_dtype(dtype)).element_size()
 
 
 def st_dtype(t: torch.dtype) -> str:
-    if t not in _NAME_OF:
-        raise H3TError(f"torch dtype {t} has no safetensors name")
-    return _NAME_OF[t]
+    try:
+        return _ST_NAME[t]
+    except KeyError:
+        raise H3TError(f"torch dtype {t} has no safetensors name") from None
 
 
 def nbytes_of(dtype: str, shape: Sequence[int]) -> int:
-    return math.prod(shape) * itemsize(dtype)
+    return itemsize(dtype) * math.prod(shape)
 
 
-def _up(v: int, a: int) -> int:
+def _ceil(v: int, a: int) -> int:
     return -(-v // a) * a
 
 
-# ------------------------------------------------------------------------------------------------ safetensors header
+def _compact(v) -> str:
+    return json.dumps(v, separators=(",", ":"))
+
+
+# ------------------------------------------------------------------------------------------------ canonical order
+def _lin(prefix: str) -> Tuple[str, ...]:
+    return tuple(f"{prefix}.{p}" for p in QUANT_PARTS)
+
+
+# Inside a block, then among the globals: these names first, in this order; every other name after them, sorted.
+_BLOCK_FIRST = ("adaln_proj.linear.weight", "adaln_proj.linear.bias", "norm1.weight", "attn.q_norm.weight",
+                "attn.k_norm.weight", *_lin("attn.qkv_proj"), *_lin("attn.out_proj"), "norm2.weight",
+                *_lin("mlp.fc1"), *_lin("mlp.fc2"))
+_GLOBAL_FIRST = ("video_patch_proj.weight", "video_patch_proj.bias", "audio_patch_proj.weight", "audio_patch_proj.bias",
+                 "condition_proj.weight", "condition_proj.bias", "adaln_t_table", "rope.inv_freq",
+                 "final_layer.norm.weight", "final_layer.adaln_proj.linear.weight",
+                 "final_layer.adaln_proj.linear.bias", "final_layer.video_out.weight", "final_layer.video_out.bias",
+                 "final_layer.audio_out.weight", "final_layer.audio_out.bias")
+_REFINER_TAIL_FIRST = ("token_refiner.final_norm.weight",)
+# what the whole-model forward needs from the globals (adaln_t_table is optional)
+_GLOBALS_NEEDED = tuple(n for n in _GLOBAL_FIRST if n != "adaln_t_table")
+
+_IN_BLOCK = re.compile(r"blocks\.(\d+)\.(.+)")
+_IN_REFINER = re.compile(r"token_refiner\.blocks\.(\d+)\.(.+)")
+
+
+def _canonical(names: Iterable[str], first: Sequence[str]) -> List[str]:
+    rank = {n: i for i, n in enumerate(first)}
+    return sorted(names, key=lambda n: (0, rank[n], "") if n in rank else (1, 0, n))
+
+
+def quant_linear_names(names: Iterable[str]) -> List[str]:
+    """The W4A8 linears among a block's tensor names: the prefixes that carry a codebook."""
+    have = set(names)
+    return [p for p in LINEARS if f"{p}.weight_codebook" in have]
+
+
+# ------------------------------------------------------------------------------------------------ layout plan
+@dataclass(frozen=True)
+class Slot:
+    """One tensor's place: offset from the data section (globals) or from the block start (block slots)."""
+    name: str
+    dtype: str
+    shape: Tuple[int, ...]
+    offset: int
+    nbytes: int
+
+    def row(self) -> list:
+        return [self.name, self.dtype, list(self.shape), self.offset, self.nbytes]
+
+
+BlockEntry = Slot  # the reader's name for a block slot
+
+
+def _place(specs: Sequence[Tuple[str, str, Tuple[int, ...]]]) -> Tuple[List[Slot], int]:
+    """Slots for the tensors in order, each at the next TENSOR_ALIGN boundary from 0; and the end offset."""
+    slots, end = [], 0
+    for name, dt, shape in specs:
+        at = _ceil(end, TENSOR_ALIGN)
+        slots.append(Slot(name, dt, tuple(shape), at, nbytes_of(dt, shape)))
+        end = at + slots[-1].nbytes
+    return slots, end
+
+
+class Plan:
+    """Where every tensor of a checkpoint goes in its .h3t file: the globals region, then N equal blocks."""
+
+    def __init__(self, cfg: H3Config, specs: Mapping[str, Tuple[str, Tuple[int, ...]]]):
+        glob, refiner, refiner_tail, blocks = [], {}, [], {}
+        for name in specs:
+            if name.startswith(PAD_PREFIX):
+                raise H3TError(f"tensor {name!r} uses the reserved padding prefix {PAD_PREFIX!r}")
+            m = _IN_BLOCK.fullmatch(name)
+            if m:
+                blocks.setdefault(int(m.group(1)), set()).add(m.group(2))
+                continue
+            m = _IN_REFINER.fullmatch(name)
+            if m:
+                refiner.setdefault(int(m.group(1)), []).append(m.group(2))
+            elif name.startswith("token_refiner."):
+                refiner_tail.append(name)
+            else:
+                glob.append(name)
+        self.n_blocks = cfg.layers
+        if self.n_blocks < 1 or sorted(blocks) != list(range(self.n_blocks)):
+            raise H3TError(f"the config has {self.n_blocks} blocks, the tensors carry block indices "
+                           f"{sorted(blocks)[:8]}")
+        rel = _canonical(blocks[0], _BLOCK_FIRST)
+        sig0 = {r: specs[f"blocks.0.{r}"] for r in rel}
+        for i in range(1, self.n_blocks):
+            if blocks[i] != blocks[0]:
+                raise H3TError(f"block {i}'s tensor set differs from block 0: missing "
+                               f"{sorted(blocks[0] - blocks[i])[:4]}, extra {sorted(blocks[i] - blocks[0])[:4]}")
+            for r in rel:
+                dt, shape = specs[f"blocks.{i}.{r}"]
+                if (dt, tuple(shape)) != (sig0[r][0], tuple(sig0[r][1])):
+                    raise H3TError(f"blocks.{i}.{r} is {dt}{tuple(shape)}, block 0 has {sig0[r][0]}{tuple(sig0[r][1])}")
+        self.block, end = _place([(r, sig0[r][0], sig0[r][1]) for r in rel])
+        self.block_nbytes = _ceil(end, BLOCK_ALIGN)
+        order = _canonical(glob, _GLOBAL_FIRST)
+        for j in sorted(refiner):
+            order += [f"token_refiner.blocks.{j}.{r}" for r in _canonical(refiner[j], _BLOCK_FIRST)]
+        order += _canonical(refiner_tail, _REFINER_TAIL_FIRST)
+        self.globals, end = _place([(n, specs[n][0], specs[n][1]) for n in order])
+        self.blocks_start = _ceil(end, BLOCK_ALIGN)
+        self.data_end = self.blocks_start + self.n_blocks * self.block_nbytes
+
+    def block_start(self, i: int) -> int:
+        return self.blocks_start + i * self.block_nbytes
+
+    def placements(self) -> List[Tuple[int, str, int]]:
+        """(offset, name, nbytes) of every tensor and every padding run, in file order, covering [0, data_end)."""
+        tensors = [(s.offset, s.name, s.nbytes) for s in self.globals]
+        for i in range(self.n_blocks):
+            tensors += [(self.block_start(i) + s.offset, f"blocks.{i}.{s.name}", s.nbytes) for s in self.block]
+        out, at, pads = [], 0, 0
+        for off, name, nb in sorted(tensors, key=lambda t: t[0]) + [(self.data_end, None, 0)]:
+            if off > at:
+                out.append((at, f"{PAD_PREFIX}{pads}", off - at))
+                pads += 1
+            if name is not None:
+                out.append((off, name, nb))
+            at = off + nb
+        return out
+
+    def metadata(self, cfg: H3Config, quant: Mapping[str, object], source_name: str, source_size: int,
+                 source_sha256: str) -> Dict[str, str]:
+        ranges = [[self.block_start(i), self.block_start(i) + self.block_nbytes] for i in range(self.n_blocks)]
+        return {"format": FORMAT, "version": str(VERSION), "config": cfg.to_json(), "n_blocks": str(self.n_blocks),
+                "tensor_align": str(TENSOR_ALIGN), "block_align": str(BLOCK_ALIGN),
+                "block_nbytes": str(self.block_nbytes), "blocks_start": str(self.blocks_start),
+                "block_ranges": _compact(ranges), "block_layout": _compact([s.row() for s in self.block]),
+                "globals_layout": _compact([s.row() for s in self.globals]),
+                "quant": json.dumps(dict(quant), sort_keys=True), "source_name": source_name,
+                "source_size": str(source_size), "source_header_sha256": source_sha256}
+
+
+# ------------------------------------------------------------------------------------------------ header
 class Header(NamedTuple):
-    tensors: Dict[str, dict]  # name -> {"dtype", "shape", "data_offsets"} (offsets from the data section start)
+    tensors: Dict[str, dict]  # name -> {"dtype", "shape", "data_offsets"} (offsets from the data section)
     meta: Dict[str, str]
     data_start: int
     file_size: int
@@ -106,47 +234,52 @@ class Header(NamedTuple):
 
 
 def read_header(path: Union[str, os.PathLike]) -> Header:
-    """The safetensors header of `path`, checked against the file: every entry inside the data section, byte counts
-    matching dtype x shape.  Tensor data is not read."""
+    """The safetensors header of `path`, each entry checked to lie in the data section with dtype x shape bytes.
+    Reads no tensor data."""
     size = os.path.getsize(path)
-    with open(path, "rb") as f:
-        lead = f.read(8)
-        if len(lead) < 8:
-            raise H3TError(f"{path}: {size} bytes is too small for a safetensors file")
-        (n,) = struct.unpack("<Q", lead)
-        if n > _HEADER_CAP or 8 + n > size:
-            raise H3TError(f"{path}: header size {n} does not fit the {size}-byte file")
-        raw = f.read(n)
-    if not raw.lstrip(b" ").startswith(b"{"):
-        raise H3TError(f"{path}: the safetensors header is not a JSON object")
+    with open(path, "rb") as fh:
+        prefix = fh.read(8)
+        n = struct.unpack("<Q", prefix)[0] if len(prefix) == 8 else -1
+        if n < 0 or n > _MAX_HEADER or 8 + n > size:
+            raise H3TError(f"{path}: not a safetensors file ({size} bytes, header length field {n})")
+        blob = fh.read(n)
     try:
-        table = json.loads(raw)
+        table = json.loads(blob)
     except ValueError as e:
         raise H3TError(f"{path}: the safetensors header is not valid JSON: {e}") from None
     if not isinstance(table, dict):
         raise H3TError(f"{path}: the safetensors header is not a JSON object")
     meta = table.pop("__metadata__", None) or {}
-    data_len = size - 8 - n
+    room = size - 8 - n
     for name, e in table.items():
         try:
-            a, b = e["data_offsets"]
-            dtype, shape = e["dtype"], e["shape"]
+            lo, hi = e["data_offsets"]
+            dt, shape = e["dtype"], e["shape"]
         except (KeyError, TypeError, ValueError):
             raise H3TError(f"{path}: header entry {name!r} is malformed") from None
-        if not 0 <= a <= b <= data_len:
-            raise H3TError(f"{path}: {name!r} spans [{a}, {b}), outside the {data_len}-byte data section "
+        if not 0 <= lo <= hi <= room:
+            raise H3TError(f"{path}: {name!r} spans [{lo}, {hi}), outside the {room}-byte data section "
                            "(truncated file?)")
-        if dtype in _DT and b - a != nbytes_of(dtype, shape):
-            raise H3TError(f"{path}: {name!r} holds {b - a} bytes, {dtype}{list(shape)} needs {nbytes_of(dtype, shape)}")
-    return Header(table, meta, 8 + n, size, raw)
+        if dt in _TORCH and hi - lo != nbytes_of(dt, shape):
+            raise H3TError(f"{path}: {name!r} holds {hi - lo} bytes, {dt}{list(shape)} needs {nbytes_of(dt, shape)}")
+    return Header(table, meta, 8 + n, size, blob)
 
 
-class BlockEntry(NamedTuple):
-    name: str  # relative to the block
-    dtype: str
-    shape: Tuple[int, ...]
-    offset: int  # from the block start
-    nbytes: int
+# ------------------------------------------------------------------------------------------------ weights from views
+def _weights(view: Callable[[str], Optional[torch.Tensor]], group: int, convrot: int) -> BlockWeights:
+    """BlockWeights from a name -> tensor accessor (None when absent): a linear with a codebook is W4A8."""
+
+    def linear(p: str) -> Weight:
+        book = view(f"{p}.weight_codebook")
+        if book is None:
+            return view(f"{p}.weight")
+        return W4A8Weight(view(f"{p}.weight"), view(f"{p}.weight_s_rel"), view(f"{p}.weight_s_channel"), book,
+                          group, convrot)
+
+    return BlockWeights(qkv=linear("attn.qkv_proj"), out=linear("attn.out_proj"), fc1=linear("mlp.fc1"),
+                        fc2=linear("mlp.fc2"), norm1=view("norm1.weight"), norm2=view("norm2.weight"),
+                        q_norm=view("attn.q_norm.weight"), k_norm=view("attn.k_norm.weight"),
+                        adaln_w=view("adaln_proj.linear.weight"), adaln_b=view("adaln_proj.linear.bias"))
 
 
 class TensorInfo(NamedTuple):
@@ -156,185 +289,158 @@ class TensorInfo(NamedTuple):
     nbytes: int
 
 
-def quant_linear_names(names: Iterable[str]) -> List[str]:
-    """The W4A8 linears (prefixes) present among a block's tensor names: those with a codebook."""
-    have = set(names)
-    return [p for p in LINEARS if f"{p}.weight_codebook" in have]
-
-
-def typed_view(buf: torch.Tensor, offset: int, dtype: str, shape: Sequence[int]) -> torch.Tensor:
-    """Zero-copy `dtype[shape]` view at byte `offset` of a 1-D uint8 tensor (any device)."""
-    v = buf[offset:offset + nbytes_of(dtype, shape)]
-    t = torch_dtype(dtype)
-    return (v if t is torch.uint8 else v.view(t)).view(tuple(shape))
-
-
-def build_block_weights(get: Callable[[str], torch.Tensor], has: Callable[[str], bool], group: int, convrot: int,
-                        adaln: bool = True) -> BlockWeights:
-    """BlockWeights from a block-relative name accessor: a linear with a codebook is W4A8, else dense."""
-
-    def linear(p: str) -> Weight:
-        if has(f"{p}.weight_codebook"):
-            return W4A8Weight(get(f"{p}.weight"), get(f"{p}.weight_s_rel"), get(f"{p}.weight_s_channel"),
-                              get(f"{p}.weight_codebook"), group, convrot)
-        return get(f"{p}.weight")
-
-    mod = adaln and has("adaln_proj.linear.weight")
-    return BlockWeights(qkv=linear("attn.qkv_proj"), out=linear("attn.out_proj"), fc1=linear("mlp.fc1"),
-                        fc2=linear("mlp.fc2"), norm1=get("norm1.weight"), norm2=get("norm2.weight"),
-                        q_norm=get("attn.q_norm.weight"), k_norm=get("attn.k_norm.weight"),
-                        adaln_w=get("adaln_proj.linear.weight") if mod else None,
-                        adaln_b=get("adaln_proj.linear.bias") if mod else None)
-
-
-_GLOBALS_NEEDED = ("video_patch_proj.weight", "video_patch_proj.bias", "audio_patch_proj.weight",
-                   "audio_patch_proj.bias", "condition_proj.weight", "condition_proj.bias", "rope.inv_freq",
-                   "final_layer.norm.weight", "final_layer.adaln_proj.linear.weight",
-                   "final_layer.adaln_proj.linear.bias", "final_layer.video_out.weight", "final_layer.video_out.bias",
-                   "final_layer.audio_out.weight", "final_layer.audio_out.bias")
-
-
 # ------------------------------------------------------------------------------------------------ reader
 class H3TFile:
-    """A read-only memory-mapped .h3t file (h3turbo/h3/store.py:182-400).  Every accessor returns a zero-copy view of
-    the mapping; never write into one.  The store interface of the streaming engine: n_blocks, block_nbytes,
-    block_tensor(i), block_bytes(i), block_weights_from(buf)."""
+    """A read-only, memory-mapped .h3t file (the reader of h3turbo/h3/store.py:182-400).  Every accessor hands out a
+    zero-copy view of the mapping; views stay valid after close().  As a block source of the streaming engine it has
+    n_blocks, block_nbytes, block_tensor(i), block_bytes(i) and block_weights_from(buf)."""
 
-    pinned = False  # the mapping is pageable: the streaming engine stages or pins copies of its blocks
+    pinned = False  # file pages are pageable: the engine stages or pins copies of the blocks
 
     def __init__(self, path: Union[str, os.PathLike]):
         self.path = os.fspath(path)
         hdr = read_header(self.path)
-        m = hdr.meta
-        if m.get("format") != FORMAT:
-            raise H3TError(f"{self.path}: not an h3t file (format tag {m.get('format')!r}, expected {FORMAT!r})")
+        meta = hdr.meta
+        if meta.get("format") != FORMAT:
+            raise H3TError(f"{self.path}: not an h3t file (format tag {meta.get('format')!r}, expected {FORMAT!r})")
+        if meta.get("version") != str(VERSION):
+            raise H3TError(f"{self.path}: h3t version {meta.get('version')!r}, this reader reads version {VERSION}")
         try:
-            version = int(m.get("version", "0"))
-        except (TypeError, ValueError):
-            version = -1
-        if version != VERSION:
-            raise H3TError(f"{self.path}: unsupported h3t version {m.get('version')!r} (this reader reads {VERSION})")
-        try:
-            self.cfg = H3Config.from_json(m["config"])
-            self.n_blocks = int(m["n_blocks"])
-            self.block_nbytes = int(m["block_nbytes"])
-            self.blocks_start = int(m["blocks_start"])
-            self.block_layout = [BlockEntry(n, d, tuple(s), int(o), int(b)) for n, d, s, o, b in json.loads(m["block_layout"])]
-            self.quant = json.loads(m.get("quant") or "{}")
-            self.meta = dict(m)
-            self.source_name = m.get("source_name", "")
-            self.source_size = int(m.get("source_size") or 0)
-            self.data_start, self.file_size = hdr.data_start, hdr.file_size
-            self._check(hdr)
+            self.cfg = H3Config.from_json(meta["config"])
+            self.n_blocks = int(meta["n_blocks"])
+            self.block_nbytes = int(meta["block_nbytes"])
+            self.blocks_start = int(meta["blocks_start"])
+            self.block_layout = [Slot(n, d, tuple(s), int(o), int(b)) for n, d, s, o, b in json.loads(meta["block_layout"])]
+            ranges = json.loads(meta["block_ranges"])
+            self.quant = json.loads(meta.get("quant") or "{}")
+            self.source_name = meta.get("source_name", "")
+            self.source_size = int(meta.get("source_size") or 0)
+            self.meta = dict(meta)
+            self.layout = BlockLayout([LayoutEntry(s.name, torch_dtype(s.dtype), s.shape, s.offset, s.nbytes)
+                                       for s in self.block_layout])
         except H3TError:
             raise
-        except (KeyError, TypeError, ValueError, IndexError) as e:
+        except (KeyError, TypeError, ValueError, IndexError, AttributeError) as e:
             raise H3TError(f"{self.path}: corrupt h3t metadata: {e!r}") from None
+        self.data_start, self.file_size = hdr.data_start, hdr.file_size
+        self._verify(hdr, ranges)
         self.quant_group = int(self.quant.get("group_size", self.cfg.quant_group))
         self.quant_convrot = int(self.quant.get("convrot_groupsize", self.cfg.quant_convrot))
-        self._layout = {e.name: e for e in self.block_layout}
-        self._info = {name: TensorInfo(e["dtype"], tuple(e["shape"]), self.data_start + e["data_offsets"][0],
-                                       e["data_offsets"][1] - e["data_offsets"][0])
-                      for name, e in hdr.tensors.items() if not name.startswith(PAD_PREFIX)}
+        self._info = {n: TensorInfo(e["dtype"], tuple(e["shape"]), self.data_start + e["data_offsets"][0],
+                                    e["data_offsets"][1] - e["data_offsets"][0])
+                      for n, e in hdr.tensors.items() if not n.startswith(PAD_PREFIX)}
         with open(self.path, "rb") as fh:
-            self._mm: Optional[mmap.mmap] = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
-        self._np: Optional[np.ndarray] = np.frombuffer(self._mm, dtype=np.uint8)
-        with warnings.catch_warnings():  # torch notes the buffer is read-only; nothing here writes to it
+            self._map: Optional[mmap.mmap] = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+        with warnings.catch_warnings():  # the mapping is read-only; nothing here writes through these views
             warnings.simplefilter("ignore")
-            self._u8: Optional[torch.Tensor] = torch.frombuffer(self._mm, dtype=torch.uint8)
+            self._bytes: Optional[torch.Tensor] = torch.frombuffer(self._map, dtype=torch.uint8)
 
-    def _check(self, hdr: Header) -> None:
+    def _verify(self, hdr: Header, ranges) -> None:
+        """The format's invariants, against the header: block count, alignment, exact size, contiguity, the shared
+        block layout, complete W4A8 linears."""
         p = self.path
         if self.n_blocks < 1 or self.n_blocks != self.cfg.layers:
             raise H3TError(f"{p}: n_blocks={self.n_blocks} but config.layers={self.cfg.layers}")
-        if self.data_start % BLOCK_ALIGN or self.blocks_start % BLOCK_ALIGN or self.block_nbytes % BLOCK_ALIGN:
+        if any(v % BLOCK_ALIGN for v in (self.data_start, self.blocks_start, self.block_nbytes)):
             raise H3TError(f"{p}: data section or block offsets are not {BLOCK_ALIGN}-byte aligned")
-        need = self.data_start + self.blocks_start + self.n_blocks * self.block_nbytes
-        if hdr.file_size != need:
-            raise H3TError(f"{p}: the layout needs exactly {need} bytes, the file has {hdr.file_size} "
+        want = self.data_start + self.blocks_start + self.n_blocks * self.block_nbytes
+        if hdr.file_size != want:
+            raise H3TError(f"{p}: the layout needs exactly {want} bytes, the file has {hdr.file_size} "
                            "(truncated, or trailing data)")
-        ranges = json.loads(hdr.meta["block_ranges"])
         if not isinstance(ranges, list) or len(ranges) != self.n_blocks:
             raise H3TError(f"{p}: block_ranges does not list {self.n_blocks} blocks")
-        for i, (a, b) in enumerate(ranges):
-            if a != self.blocks_start + i * self.block_nbytes or b - a != self.block_nbytes:
-                raise H3TError(f"{p}: block_ranges[{i}] = [{a}, {b}) disagrees with blocks_start / block_nbytes")
-        for i in range(self.n_blocks):  # header entries of every block against the shared layout
-            base = self.blocks_start + i * self.block_nbytes
-            for e in self.block_layout:
-                got = hdr.tensors.get(f"blocks.{i}.{e.name}")
-                if (got is None or got["dtype"] != e.dtype or tuple(got["shape"]) != e.shape
-                        or list(got["data_offsets"]) != [base + e.offset, base + e.offset + e.nbytes]):
-                    raise H3TError(f"{p}: blocks.{i}.{e.name} does not match the block layout")
-        pos = 0
+        for i, r in enumerate(ranges):
+            lo = self.blocks_start + i * self.block_nbytes
+            if not isinstance(r, list) or r != [lo, lo + self.block_nbytes]:
+                raise H3TError(f"{p}: block_ranges[{i}] = {r} disagrees with blocks_start / block_nbytes")
+        if self.layout.nbytes > self.block_nbytes:
+            raise H3TError(f"{p}: the block layout spans {self.layout.nbytes} bytes, blocks are {self.block_nbytes}")
+        for i in range(self.n_blocks):
+            lo = self.blocks_start + i * self.block_nbytes
+            for s in self.block_layout:
+                e = hdr.tensors.get(f"blocks.{i}.{s.name}")
+                if (e is None or e["dtype"] != s.dtype or tuple(e["shape"]) != s.shape
+                        or list(e["data_offsets"]) != [lo + s.offset, lo + s.offset + s.nbytes]):
+                    raise H3TError(f"{p}: blocks.{i}.{s.name} does not match the block layout")
+        at = 0
         for name, e in sorted(hdr.tensors.items(), key=lambda kv: kv[1]["data_offsets"][0]):
-            a, b = e["data_offsets"]
-            if a != pos:
+            lo, hi = e["data_offsets"]
+            if lo != at:
                 raise H3TError(f"{p}: hole or overlap before {name!r}")
-            if a % TENSOR_ALIGN and not name.startswith(PAD_PREFIX):
-                raise H3TError(f"{p}: {name!r} starts at {a}, not {TENSOR_ALIGN}-byte aligned")
-            pos = b
-        if pos != hdr.file_size - self.data_start:
-            raise H3TError(f"{p}: the tensors cover {pos} of the {hdr.file_size - self.data_start} data bytes")
-        have = {e.name for e in self.block_layout}
-        for lin in quant_linear_names(have):
-            missing = [part for part in QUANT_PARTS if f"{lin}.{part}" not in have]
-            if missing:
-                raise H3TError(f"{p}: W4A8 linear {lin} lacks {missing}")
+            if lo % TENSOR_ALIGN and not name.startswith(PAD_PREFIX):
+                raise H3TError(f"{p}: {name!r} starts at {lo}, not {TENSOR_ALIGN}-byte aligned")
+            at = hi
+        if at != hdr.file_size - self.data_start:
+            raise H3TError(f"{p}: the tensors cover {at} of the {hdr.file_size - self.data_start} data bytes")
+        names = {s.name for s in self.block_layout}
+        for lin in quant_linear_names(names):
+            absent = [q for q in QUANT_PARTS if f"{lin}.{q}" not in names]
+            if absent:
+                raise H3TError(f"{p}: W4A8 linear {lin} lacks {absent}")
 
-    def _open(self) -> None:
-        if self._mm is None:
+    def _mapped(self) -> torch.Tensor:
+        if self._bytes is None:
             raise ValueError("H3TFile is closed")
+        return self._bytes
 
-    # ---- raw block bytes
+    # ---- blocks
     def block_range(self, i: int) -> Tuple[int, int]:
         """[start, end) file offsets of block i."""
         if not 0 <= i < self.n_blocks:
             raise IndexError(f"block {i} outside [0, {self.n_blocks})")
-        a = self.data_start + self.blocks_start + i * self.block_nbytes
-        return a, a + self.block_nbytes
-
-    def block_bytes(self, i: int) -> np.ndarray:
-        """Read-only uint8 numpy view of block i."""
-        self._open()
-        a, b = self.block_range(i)
-        return self._np[a:b]
+        lo = self.data_start + self.blocks_start + i * self.block_nbytes
+        return lo, lo + self.block_nbytes
 
     def block_tensor(self, i: int) -> torch.Tensor:
-        """uint8 torch view of block i: the source of a host -> device block copy."""
-        self._open()
-        a, b = self.block_range(i)
-        return self._u8[a:b]
+        """uint8 view of block i: the source of its host -> device copy."""
+        lo, hi = self.block_range(i)
+        return self._mapped()[lo:hi]
+
+    def block_bytes(self, i: int) -> np.ndarray:
+        """Read-only numpy view of block i."""
+        a = self.block_tensor(i).numpy()
+        a.flags.writeable = False
+        return a
 
     @property
     def block_layout_size(self) -> int:
-        return self.block_layout[-1].offset + self.block_layout[-1].nbytes
+        return max((s.offset + s.nbytes for s in self.block_layout), default=0)
 
-    # ---- typed tensors
+    def block_weights_from(self, buf: torch.Tensor) -> BlockWeights:
+        """Typed zero-copy views of one block held in `buf` (1-D uint8 of block_nbytes, any device)."""
+        if buf.dtype != torch.uint8 or buf.dim() != 1 or buf.numel() != self.block_nbytes:
+            raise ValueError(f"need a 1-D uint8 buffer of {self.block_nbytes} bytes, got {tuple(buf.shape)} {buf.dtype}")
+        lay = self.layout
+        return _weights(lambda n: lay.view(buf, n) if n in lay else None, self.quant_group, self.quant_convrot)
+
+    def block_weights_cpu(self, i: int) -> BlockWeights:
+        return self.block_weights_from(self.block_tensor(i))
+
+    # ---- named tensors
     def keys(self) -> List[str]:
         return list(self._info)
 
     def info(self, name: str) -> TensorInfo:
-        if name not in self._info:
-            raise KeyError(f"{name!r} is not in {self.path}")
-        return self._info[name]
+        try:
+            return self._info[name]
+        except KeyError:
+            raise KeyError(f"{name!r} is not in {self.path}") from None
 
     def tensor(self, name: str) -> torch.Tensor:
         """Zero-copy CPU view of one tensor."""
-        self._open()
         t = self.info(name)
-        return typed_view(self._u8, t.start, t.dtype, t.shape)
+        v = self._mapped()[t.start:t.start + t.nbytes]
+        dt = torch_dtype(t.dtype)
+        return (v if dt == torch.uint8 else v.view(dt)).view(t.shape)
 
-    def block_weights_from(self, buf: torch.Tensor) -> BlockWeights:
-        """Typed zero-copy views of a block held in `buf` (1-D uint8, block_nbytes long, any device)."""
-        if buf.dtype != torch.uint8 or buf.dim() != 1 or buf.numel() != self.block_nbytes:
-            raise ValueError(f"need a 1-D uint8 buffer of {self.block_nbytes} bytes, got {tuple(buf.shape)} {buf.dtype}")
-        lay = self._layout
-        return build_block_weights(lambda r: typed_view(buf, lay[r].offset, lay[r].dtype, lay[r].shape),
-                                   lay.__contains__, self.quant_group, self.quant_convrot)
+    def has_globals(self) -> bool:
+        """Whether the file holds every global tensor the whole-model forward needs."""
+        return all(n in self._info for n in _GLOBALS_NEEDED)
 
-    def block_weights_cpu(self, i: int) -> BlockWeights:
-        return self.block_weights_from(self.block_tensor(i))
+    def globals_nbytes(self, refiner: bool = True) -> int:
+        """Bytes of the tensors outside the blocks (with or without the token refiner)."""
+        return sum(t.nbytes for n, t in self._info.items()
+                   if not _IN_BLOCK.fullmatch(n) and (refiner or not n.startswith("token_refiner.")))
 
     def load_globals(self, device="cpu", *, refiner_device=None) -> GlobalWeights:
         """GlobalWeights on `device`, the token refiner on `refiner_device` (default: the same) (reference
@@ -342,52 +448,43 @@ class H3TFile:
         the mapping; refiner_device="cpu" keeps the refiner out of HBM until the text is encoded."""
         dev = torch.device(device)
         rdev = torch.device(refiner_device) if refiner_device is not None else dev
+        absent = [n for n in _GLOBALS_NEEDED if n not in self._info]
+        if absent:
+            raise H3TError(f"{self.path}: missing global tensors {absent}")
 
-        def get(name: str, d: torch.device = dev, view: bool = False) -> torch.Tensor:
+        def on(name: str, d: torch.device, keep_view: bool) -> torch.Tensor:
             t = self.tensor(name)
-            if d.type != "cpu":
-                return t.to(d)
-            return t if view else t.clone()
+            return t.to(d) if d.type != "cpu" else (t if keep_view else t.clone())
 
-        missing = [n for n in _GLOBALS_NEEDED if n not in self._info]
-        if missing:
-            raise H3TError(f"{self.path}: missing global tensors {missing}")
+        g = lambda name: on(name, dev, False)  # noqa: E731
         refiner = []
         for j in range(self.cfg.refiner_layers):
             pre = f"token_refiner.blocks.{j}."
-            refiner.append(build_block_weights(lambda r, pre=pre: get(pre + r, rdev, True),
-                                               lambda r, pre=pre: pre + r in self._info, self.quant_group,
-                                               self.quant_convrot, adaln=False))
+            w = _weights(lambda r: on(pre + r, rdev, True) if pre + r in self._info else None, self.quant_group,
+                         self.quant_convrot)
+            refiner.append(dataclasses.replace(w, adaln_w=None, adaln_b=None))  # refiner blocks are unmodulated
         fnorm = "token_refiner.final_norm.weight"
         return GlobalWeights(
-            video_patch_w=get("video_patch_proj.weight"), video_patch_b=get("video_patch_proj.bias"),
-            audio_patch_w=get("audio_patch_proj.weight"), audio_patch_b=get("audio_patch_proj.bias"),
-            condition_w=get("condition_proj.weight"), condition_b=get("condition_proj.bias"),
-            adaln_t_table=get("adaln_t_table") if "adaln_t_table" in self._info else None,
-            rope_inv_freq=get("rope.inv_freq"), final_norm=get("final_layer.norm.weight"),
-            final_adaln_w=get("final_layer.adaln_proj.linear.weight"),
-            final_adaln_b=get("final_layer.adaln_proj.linear.bias"),
-            video_out_w=get("final_layer.video_out.weight"), video_out_b=get("final_layer.video_out.bias"),
-            audio_out_w=get("final_layer.audio_out.weight"), audio_out_b=get("final_layer.audio_out.bias"),
-            refiner=refiner, refiner_final_norm=get(fnorm, rdev, True) if fnorm in self._info else None)
-
-    def has_globals(self) -> bool:
-        """Whether the file holds every global tensor the whole-model forward needs."""
-        return all(n in self._info for n in _GLOBALS_NEEDED)
-
-    def globals_nbytes(self, refiner: bool = True) -> int:
-        """Bytes of the tensors outside the blocks (the token refiner optional)."""
-        return sum(t.nbytes for n, t in self._info.items()
-                   if not _BLOCK_NAME.match(n) and (refiner or not n.startswith("token_refiner.")))
+            video_patch_w=g("video_patch_proj.weight"), video_patch_b=g("video_patch_proj.bias"),
+            audio_patch_w=g("audio_patch_proj.weight"), audio_patch_b=g("audio_patch_proj.bias"),
+            condition_w=g("condition_proj.weight"), condition_b=g("condition_proj.bias"),
+            adaln_t_table=g("adaln_t_table") if "adaln_t_table" in self._info else None,
+            rope_inv_freq=g("rope.inv_freq"), final_norm=g("final_layer.norm.weight"),
+            final_adaln_w=g("final_layer.adaln_proj.linear.weight"),
+            final_adaln_b=g("final_layer.adaln_proj.linear.bias"),
+            video_out_w=g("final_layer.video_out.weight"), video_out_b=g("final_layer.video_out.bias"),
+            audio_out_w=g("final_layer.audio_out.weight"), audio_out_b=g("final_layer.audio_out.bias"),
+            refiner=refiner, refiner_final_norm=on(fnorm, rdev, True) if fnorm in self._info else None)
 
     # ---- lifecycle
     def close(self) -> None:
-        if self._mm is None:
+        """Release the mapping (views already handed out keep it alive until they go)."""
+        if self._map is None:
             return
-        mm, self._mm, self._np, self._u8 = self._mm, None, None, None
+        m, self._map, self._bytes = self._map, None, None
         try:
-            mm.close()
-        except BufferError:  # views handed out are alive: the mapping goes away with the last of them
+            m.close()
+        except BufferError:  # live views: the mapping goes with the last of them
             pass
 
     def __enter__(self) -> "H3TFile":
@@ -408,7 +505,7 @@ class H3TFile:
 
 # ------------------------------------------------------------------------------------------------ writer
 class TensorSource:
-    """The little-endian bytes of one tensor, produced in chunks (a writer holds one chunk at a time)."""
+    """The little-endian bytes of one tensor, produced in chunks: the writer holds one chunk at a time."""
 
     dtype: str
     shape: Tuple[int, ...]
@@ -418,40 +515,40 @@ class TensorSource:
         raise NotImplementedError
 
     def read(self) -> torch.Tensor:
-        data = bytearray(self.nbytes)
-        pos = 0
+        buf = torch.empty(self.nbytes, dtype=torch.uint8)
+        at = 0
         for c in self.chunks(32 << 20):
-            data[pos:pos + len(c)] = c
-            pos += len(c)
-        buf = torch.frombuffer(data, dtype=torch.uint8) if self.nbytes else torch.empty(0, dtype=torch.uint8)
-        return typed_view(buf, 0, self.dtype, self.shape)
+            buf[at:at + len(c)] = torch.frombuffer(bytearray(c), dtype=torch.uint8)
+            at += len(c)
+        dt = torch_dtype(self.dtype)
+        return (buf if dt == torch.uint8 else buf.view(dt)).view(self.shape)
 
 
 class TorchSource(TensorSource):
     def __init__(self, t: torch.Tensor):
-        t = t.detach().cpu().contiguous()
-        self._t, self.dtype, self.shape = t, st_dtype(t.dtype), tuple(t.shape)
-        self.nbytes = t.numel() * t.element_size()
+        self._t = t.detach().cpu().contiguous()
+        self.dtype, self.shape = st_dtype(self._t.dtype), tuple(self._t.shape)
+        self.nbytes = self._t.numel() * self._t.element_size()
 
     def chunks(self, chunk_bytes: int) -> Iterator[memoryview]:
         if self.nbytes:
-            mv = memoryview(self._t.reshape(-1).view(torch.uint8).numpy())
-            for a in range(0, self.nbytes, chunk_bytes):
-                yield mv[a:a + chunk_bytes]
+            whole = memoryview(self._t.reshape(-1).view(torch.uint8).numpy())
+            for lo in range(0, self.nbytes, chunk_bytes):
+                yield whole[lo:lo + chunk_bytes]
 
 
 class LazySource(TensorSource):
-    """A tensor made by `fn()` only when it is written."""
+    """A tensor produced by `fn()` only when the writer reaches it."""
 
     def __init__(self, dtype: str, shape: Sequence[int], fn: Callable[[], torch.Tensor]):
         self.dtype, self.shape, self._fn = dtype, tuple(shape), fn
-        self.nbytes = nbytes_of(dtype, shape)
+        self.nbytes = nbytes_of(dtype, self.shape)
 
     def chunks(self, chunk_bytes: int) -> Iterator[memoryview]:
-        src = TorchSource(self._fn())
-        if (src.dtype, src.shape) != (self.dtype, self.shape):
-            raise H3TError(f"lazy tensor made {src.dtype}{src.shape}, declared {self.dtype}{self.shape}")
-        yield from src.chunks(chunk_bytes)
+        made = TorchSource(self._fn())
+        if (made.dtype, made.shape) != (self.dtype, self.shape):
+            raise H3TError(f"lazy tensor made {made.dtype}{made.shape}, declared {self.dtype}{self.shape}")
+        yield from made.chunks(chunk_bytes)
 
 
 def as_source(x: Union[TensorSource, torch.Tensor]) -> TensorSource:
@@ -462,148 +559,58 @@ def as_source(x: Union[TensorSource, torch.Tensor]) -> TensorSource:
     raise TypeError(f"expected a Tensor or TensorSource, got {type(x).__name__}")
 
 
-def _ordered(names: Iterable[str], first: Sequence[str]) -> List[str]:
-    have = set(names)
-    lead = [n for n in first if n in have]
-    return lead + sorted(have.difference(lead))
-
-
-def classify(names: Iterable[str]):
-    """(globals, {refiner block: names}, other token_refiner.* names, {block: names}); names in blocks relative."""
-    glob: List[str] = []
-    refiner: Dict[int, List[str]] = {}
-    refiner_other: List[str] = []
-    blocks: Dict[int, List[str]] = {}
-    for n in names:
-        if n.startswith(PAD_PREFIX):
-            raise H3TError(f"tensor {n!r} uses the reserved padding prefix {PAD_PREFIX!r}")
-        m = _BLOCK_NAME.match(n)
-        if m:
-            blocks.setdefault(int(m.group(1)), []).append(m.group(2))
-            continue
-        m = _REFINER_NAME.match(n)
-        if m:
-            refiner.setdefault(int(m.group(1)), []).append(m.group(2))
-        elif n.startswith("token_refiner."):
-            refiner_other.append(n)
-        else:
-            glob.append(n)
-    return glob, refiner, refiner_other, blocks
-
-
-def _pack(items: Sequence[Tuple[str, str, Tuple[int, ...]]]) -> Tuple[List[BlockEntry], int]:
-    """Each tensor at the next TENSOR_ALIGN boundary from 0, in order; returns the entries and the end offset."""
-    out, pos = [], 0
-    for name, dt, shape in items:
-        pos = _up(pos, TENSOR_ALIGN)
-        nb = nbytes_of(dt, shape)
-        out.append(BlockEntry(name, dt, tuple(shape), pos, nb))
-        pos += nb
-    return out, pos
-
-
-def _compact(v) -> str:
-    return json.dumps(v, separators=(",", ":"))
-
-
 def write_h3t(dst: Union[str, os.PathLike], cfg: H3Config, tensors: Mapping[str, Union[TensorSource, torch.Tensor]], *,
               quant: Optional[Mapping[str, object]] = None, source_name: str = "", source_size: int = 0,
               source_sha256: str = "", extra_meta: Optional[Mapping[str, str]] = None, chunk_bytes: int = 32 << 20,
               progress: Optional[Callable[[str, int, int], None]] = None) -> Dict[str, int]:
     """Write ComfyUI-layout tensors as an .h3t file (h3turbo/h3/writer.py:137-262).  The bytes go to `<dst>.part`,
-    which replaces `dst` only once complete and synced, so an interrupted write never leaves a plausible file."""
+    renamed to `dst` only once complete and synced: an interrupted write never leaves a plausible file."""
     if chunk_bytes < 4096 or chunk_bytes % 8:
         raise ValueError("chunk_bytes must be a multiple of 8, at least 4096")
-    src = {k: as_source(v) for k, v in tensors.items()}
-    glob, refiner, refiner_other, blocks = classify(src)
-    n_blocks = cfg.layers
-    if n_blocks < 1 or sorted(blocks) != list(range(n_blocks)):
-        raise H3TError(f"config has {n_blocks} blocks, the tensors carry block indices {sorted(blocks)[:8]}")
-    names0 = _ordered(blocks[0], BLOCK_ORDER)
-    sig = {r: (src[f"blocks.0.{r}"].dtype, tuple(src[f"blocks.0.{r}"].shape)) for r in names0}
-    for i in range(1, n_blocks):
-        if set(blocks[i]) != set(names0):
-            raise H3TError(f"block {i}'s tensor set differs from block 0: missing {sorted(set(names0) - set(blocks[i]))[:4]},"
-                           f" extra {sorted(set(blocks[i]) - set(names0))[:4]}")
-        for r in names0:
-            s = src[f"blocks.{i}.{r}"]
-            if (s.dtype, tuple(s.shape)) != sig[r]:
-                raise H3TError(f"blocks.{i}.{r} is {s.dtype}{tuple(s.shape)}, block 0 has {sig[r][0]}{sig[r][1]}")
-    block_layout, block_end = _pack([(r, *sig[r]) for r in names0])
-    block_nbytes = _up(block_end, BLOCK_ALIGN)
-
-    gnames = _ordered(glob, GLOBAL_ORDER)
-    for j in sorted(refiner):
-        gnames += [f"token_refiner.blocks.{j}.{r}" for r in _ordered(refiner[j], BLOCK_ORDER)]
-    gnames += _ordered(refiner_other, ("token_refiner.final_norm.weight",))
-    glob_layout, glob_end = _pack([(n, src[n].dtype, tuple(src[n].shape)) for n in gnames])
-    blocks_start = _up(glob_end, BLOCK_ALIGN)
-    data_end = blocks_start + n_blocks * block_nbytes
+    src = {name: as_source(v) for name, v in tensors.items()}
+    plan = Plan(cfg, {name: (s.dtype, s.shape) for name, s in src.items()})
     if quant:
         qmeta = dict(quant)
-    elif quant_linear_names(names0):
+    elif quant_linear_names(s.name for s in plan.block):
         qmeta = {"format": "asym_w4a8_int8", "group_size": cfg.quant_group, "convrot_groupsize": cfg.quant_convrot}
     else:
         qmeta = {}
-
-    # every byte of the data section in order: (offset, name, nbytes, source or None for padding)
-    placed = [(e.offset, e.name, e.nbytes, src[e.name]) for e in glob_layout]
-    for i in range(n_blocks):
-        base = blocks_start + i * block_nbytes
-        placed += [(base + e.offset, f"blocks.{i}.{e.name}", e.nbytes, src[f"blocks.{i}.{e.name}"]) for e in block_layout]
-    placed.sort(key=lambda it: it[0])
-    runs: List[Tuple[int, str, int, Optional[TensorSource]]] = []
-    pos, pads = 0, 0
-    for off, name, nb, s in placed + [(data_end, "", 0, None)]:
-        if off < pos:
-            raise H3TError(f"internal layout overlap at {name!r}")
-        if off > pos:
-            runs.append((pos, f"{PAD_PREFIX}{pads}", off - pos, None))
-            pads += 1
-        if name:
-            runs.append((off, name, nb, s))
-        pos = off + nb
-
-    meta = {"format": FORMAT, "version": str(VERSION), "config": cfg.to_json(), "n_blocks": str(n_blocks),
-            "tensor_align": str(TENSOR_ALIGN), "block_align": str(BLOCK_ALIGN), "block_nbytes": str(block_nbytes),
-            "blocks_start": str(blocks_start),
-            "block_ranges": _compact([[blocks_start + i * block_nbytes, blocks_start + (i + 1) * block_nbytes]
-                                      for i in range(n_blocks)]),
-            "block_layout": _compact([[e.name, e.dtype, list(e.shape), e.offset, e.nbytes] for e in block_layout]),
-            "globals_layout": _compact([[e.name, e.dtype, list(e.shape), e.offset, e.nbytes] for e in glob_layout]),
-            "quant": json.dumps(qmeta, sort_keys=True), "source_name": source_name, "source_size": str(source_size),
-            "source_header_sha256": source_sha256}
+    meta = plan.metadata(cfg, qmeta, source_name, source_size, source_sha256)
     meta.update({str(k): str(v) for k, v in (extra_meta or {}).items()})
+    runs = plan.placements()
     table: Dict[str, object] = {"__metadata__": meta}
-    for off, name, nb, s in runs:
-        table[name] = {"dtype": s.dtype if s else "U8", "shape": list(s.shape) if s else [nb], "data_offsets": [off, off + nb]}
+    for off, name, nb in runs:
+        s = src.get(name)
+        table[name] = {"dtype": s.dtype if s else "U8", "shape": list(s.shape) if s else [nb],
+                       "data_offsets": [off, off + nb]}
     head = _compact(table).encode("ascii")
-    data_start = _up(8 + len(head), BLOCK_ALIGN)
-    head += b" " * (data_start - 8 - len(head))  # JSON whitespace: aligns the data section
+    data_start = _ceil(8 + len(head), BLOCK_ALIGN)
+    head = head.ljust(data_start - 8, b" ")  # JSON whitespace aligns the data section
 
     dst = os.fspath(dst)
     part = dst + ".part"
-    payload = sum(nb for _, name, nb, _ in runs if not name.startswith(PAD_PREFIX))
-    done = 0
+    payload = sum(src[name].nbytes for _, name, _ in runs if name in src)
+    written = 0
     try:
-        with open(part, "wb") as f:
-            f.write(struct.pack("<Q", data_start - 8))
-            f.write(head)
-            for off, name, nb, s in runs:
+        with open(part, "wb") as fh:
+            fh.write(struct.pack("<Q", len(head)))
+            fh.write(head)
+            for _, name, nb in runs:
+                s = src.get(name)
                 if s is None:
-                    f.write(bytes(nb))
+                    fh.write(bytes(nb))
                     continue
-                wrote = 0
+                got = 0
                 for c in s.chunks(chunk_bytes):
-                    f.write(c)
-                    wrote += len(c)
-                if wrote != nb:
-                    raise H3TError(f"{name}: the source gave {wrote} bytes, expected {nb}")
-                done += nb
+                    fh.write(c)
+                    got += len(c)
+                if got != nb:
+                    raise H3TError(f"{name}: the source gave {got} bytes, expected {nb}")
+                written += nb
                 if progress and nb >= (1 << 20):
-                    progress(name, done, payload)
-            f.flush()
-            os.fsync(f.fileno())  # data on disk before the rename makes it visible
+                    progress(name, written, payload)
+            fh.flush()
+            os.fsync(fh.fileno())  # on disk before the rename makes it visible
         os.replace(part, dst)
     except BaseException:
         try:
@@ -611,5 +618,7 @@ def write_h3t(dst: Union[str, os.PathLike], cfg: H3Config, tensors: Mapping[str,
         except OSError:
             pass
         raise
-    return {"file_size": data_start + data_end, "data_start": data_start, "blocks_start": blocks_start,
-            "block_nbytes": block_nbytes, "n_blocks": n_blocks, "n_pads": pads, "n_tensors": len(runs) - pads}
+    n_pads = sum(1 for _, name, _ in runs if name.startswith(PAD_PREFIX))
+    return {"file_size": data_start + plan.data_end, "data_start": data_start, "blocks_start": plan.blocks_start,
+            "block_nbytes": plan.block_nbytes, "n_blocks": plan.n_blocks, "n_pads": n_pads,
+            "n_tensors": len(runs) - n_pads}
