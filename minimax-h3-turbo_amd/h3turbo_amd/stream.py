@@ -560,6 +560,16 @@ class StreamingProvider:
     def device_bytes(self) -> int:
         return (len(self._resident) + len(self._slots)) * self.store.block_nbytes
 
+    @property
+    def resident_count(self) -> int:
+        """Blocks held in HBM for good (the leading ones)."""
+        return len(self._resident)
+
+    @property
+    def ring_count(self) -> int:
+        """Ring slots the streamed blocks rotate through (0 when parked or nothing streams)."""
+        return len(self._slots)
+
     def resize(self, resident: int, ring: int = 3, *, lock_host: bool = True, ram_headroom_bytes: int = 3 * _GIB) -> int:
         """Change how many leading blocks live in HBM and how many ring slots exist, between forwards, keeping the
         host side (page-locked copies, staging buffers) so nothing is re-read from the store.  resize(r, 0) with
