@@ -10,7 +10,12 @@
 // every partial sum of <= 1024 bf16 / f16 terms is exact in fp64 unless a block spans more than ~2^37 in
 // magnitude, so the single rounding to fp32 reproduces the reference's fp64 matmul bit for bit.
 //
-// Fast path (rot = 256, bf16/f16): one wavefront per row, 4 rows per 256-thread workgroup.  A 256-block spans
+// Rotation sizes that are not powers of 4 (8, 32, 128, 512: an extension the reference rejects) use
+//   H = kron(H2, H4, ..., H4) / sqrt(rot),  H2 = [[1, 1], [1, -1]] as the most significant factor,
+// computed as the exact fp64 sum of +-x times fp64(1/sqrt(rot)) = RN(sqrt 2) * 2^-(log2(rot) + 1) / 2, then
+// rounded to fp32: one fp64 rounding (1/sqrt(rot) is irrational) and the rounding to fp32.
+//
+// Fast path (rot = 256 or 128, bf16/f16): one wavefront per row, 4 rows per 256-thread workgroup.  A 256-block spans
 // 16 lanes x 16 elements; the four base-4 digits of the in-block index are brought into registers two at a
 // time by two LDS transposes (bf16 input, then fp64 mid-values), so every butterfly is register-local.  The
 // whole row stays in registers as rounded 16-bit values until its absmax is known; x is read once and q
@@ -27,6 +32,20 @@ __device__ __forceinline__ void h4(double& a, double& b, double& c, double& d) {
   b = nb;
   c = nc;
   d = nd;
+}
+
+// y = x @ H2 on two values.
+__device__ __forceinline__ void h2(double& a, double& b) {
+  const double s = a + b, d = a - b;
+  a = s;
+  b = d;
+}
+
+constexpr double kSqrt2 = 0x1.6a09e667f3bcdp+0;  // RN(sqrt(2))
+
+// 1/sqrt(2^log2) in fp64: exact for even log2, RN(sqrt 2) * 2^-(log2 + 1) / 2 for odd log2.
+__device__ __forceinline__ double rot_scale(int log2) {
+  return (log2 & 1) ? kSqrt2 * ldexp(1.0, -(log2 + 1) / 2) : ldexp(1.0, -log2 / 2);
 }
 
 // Same, folding the final 1/16 of H256 in: every operation stays exact (power-of-two scaling).
@@ -97,7 +116,9 @@ constexpr int kMidStride = 16 * kMidRow + 4;
 // Row layout: element e of row r is at x[r * ldx + (e >> hshift) * hstride + (e & (2^hshift - 1))]; hshift = 31
 // is a plain row, hshift = log2(head_dim) reads a head-major [heads, rows, head_dim] tensor as rows of
 // heads * head_dim (head_dim >= 16, so a lane's 16 consecutive elements stay inside one head).
-template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone>
+// ROT 256, or 128: the 256 elements of a lane group are then two 128-blocks (bit 7 of the index separates them),
+// with H2 on bit 6 in place of H4 on bits 6-7, and the scale applied at the end.
+template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone, int ROT = 256>
 __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __restrict__ x, int64_t rows, int k,
                                                           int64_t ldx, int hshift, int64_t hstride,
                                                           int8_t* __restrict__ q, int64_t ldq, float* __restrict__ xs) {
@@ -165,8 +186,16 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     // (2) digit 2 (r = d2 + 4*d3) and digit 3
 #pragma unroll
     for (int d3 = 0; d3 < 4; ++d3) h4(v[4 * d3], v[4 * d3 + 1], v[4 * d3 + 2], v[4 * d3 + 3]);
+    if constexpr (ROT == 256) {
 #pragma unroll
-    for (int d2 = 0; d2 < 4; ++d2) h4(v[d2], v[d2 + 4], v[d2 + 8], v[d2 + 12]);
+      for (int d2 = 0; d2 < 4; ++d2) h4(v[d2], v[d2 + 4], v[d2 + 8], v[d2 + 12]);
+    } else {  // H2 on bit 6 of each 128-block
+#pragma unroll
+      for (int d2 = 0; d2 < 4; ++d2) {
+        h2(v[d2], v[d2 + 4]);
+        h2(v[d2 + 8], v[d2 + 12]);
+      }
+    }
     // (3) transpose the fp64 mid-values back: lane l then holds elements 16*l + j, j = 0..15 (digits 0,1 local)
     wave_lds_sync();  // the input reads above are done before the area is overwritten
 #pragma unroll
@@ -178,8 +207,15 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     // (4) digit 0 (j = d0 + 4*d1), then digit 1 with the 1/16 folded in
 #pragma unroll
     for (int d1 = 0; d1 < 4; ++d1) h4(w[4 * d1], w[4 * d1 + 1], w[4 * d1 + 2], w[4 * d1 + 3]);
+    if constexpr (ROT == 256) {
 #pragma unroll
-    for (int d0 = 0; d0 < 4; ++d0) h4_div16(w[d0], w[d0 + 4], w[d0 + 8], w[d0 + 12]);
+      for (int d0 = 0; d0 < 4; ++d0) h4_div16(w[d0], w[d0 + 4], w[d0 + 8], w[d0 + 12]);
+    } else {  // exact sums, then the one fp64 rounding of the 1/sqrt(128) scale
+#pragma unroll
+      for (int d0 = 0; d0 < 4; ++d0) h4(w[d0], w[d0 + 4], w[d0 + 8], w[d0 + 12]);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) w[j] *= kSqrt2 * 0.0625;
+    }
     // (5) one rounding to fp32, absmax, one rounding to the activation dtype
 #pragma unroll
     for (int j = 0; j < 16; j += 2) {
@@ -293,14 +329,14 @@ __device__ __forceinline__ float round_dt(float f) {
 
 template <int DT, bool EAGER, bool ROTATE_ONLY>
 __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict__ x, int64_t rows, int k, int64_t ldx,
-                                                          int log4, int8_t* __restrict__ q, int64_t ldq,
+                                                          int log2, int8_t* __restrict__ q, int64_t ldq,
                                                           float* __restrict__ xs, void* __restrict__ y, int64_t ldy) {
   __shared__ double buf[1024];
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   if (row >= rows) return;
   const int t = threadIdx.x;
-  const double scale = ldexp(1.0, -log4);  // 1/sqrt(4^log4), exact
+  const double scale = rot_scale(log2);
   float amax = 0.0f, s = 1.0f;
 
   for (int sweep = ROTATE_ONLY ? 1 : 0; sweep < 2; ++sweep) {
@@ -309,9 +345,17 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
       __syncthreads();
       for (int e = t; e < n; e += 256) buf[e] = static_cast<double>(load_x<DT>(x, row * ldx + c0 + e));
       __syncthreads();
-      for (int d = 0, S = 1; d < log4; ++d, S *= 4) {
+      int S = 1;
+      for (int d = 0; d < log2 / 2; ++d, S *= 4) {  // radix-4 stages over bit pairs, from the bottom
         const int base = (t / S) * 4 * S + (t % S);
         if (base < n) h4(buf[base], buf[base + S], buf[base + 2 * S], buf[base + 3 * S]);
+        __syncthreads();
+      }
+      if (log2 & 1) {  // the H2 stage on the top bit
+        for (int u = t; u < n / 2; u += 256) {
+          const int base = (u / S) * 2 * S + (u % S);
+          h2(buf[base], buf[base + S]);
+        }
         __syncthreads();
       }
       for (int e = t; e < n; e += 256) {
@@ -347,11 +391,11 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
 }
 
 // ------------------------------------------------------------------------------------------------ host side
-template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone>
+template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone, int ROT = 256>
 static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int hshift, int64_t hstride, int8_t* q,
                       int64_t ldq, float* xs, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>((rows + (4 / WPR) - 1) / (4 / WPR)));
-  hipLaunchKernelGGL((rotquant256_kernel<NPASS, WPR, F16, EAGER, ACT>), grid, dim3(256), 0, st,
+  hipLaunchKernelGGL((rotquant256_kernel<NPASS, WPR, F16, EAGER, ACT, ROT>), grid, dim3(256), 0, st,
                      static_cast<const uint16_t*>(x), rows, k, ldx, hshift, hstride, q, ldq, xs);
 }
 
@@ -373,13 +417,13 @@ static void rq_plan(int blocks, int64_t rows, int& npass, int& wpr) {
     }
 }
 
-template <bool F16, bool EAGER, int ACT = kActNone>
+template <bool F16, bool EAGER, int ACT = kActNone, int ROT = 256>
 static bool dispatch256(int npass, int wpr, const void* x, int64_t rows, int k, int64_t ldx, int hshift,
                         int64_t hstride, int8_t* q, int64_t ldq, float* xs, hipStream_t st) {
   switch (npass * 8 + wpr) {
 #define H3K_CASE(P, W)      \
   case P * 8 + W:           \
-    launch256<P, W, F16, EAGER, ACT>(x, rows, k, ldx, hshift, hstride, q, ldq, xs, st); \
+    launch256<P, W, F16, EAGER, ACT, ROT>(x, rows, k, ldx, hshift, hstride, q, ldq, xs, st); \
     return true;
     H3K_CASE(1, 1) H3K_CASE(2, 1) H3K_CASE(3, 1) H3K_CASE(4, 1) H3K_CASE(5, 1) H3K_CASE(6, 1) H3K_CASE(7, 1)
     H3K_CASE(8, 1) H3K_CASE(1, 4) H3K_CASE(2, 4) H3K_CASE(3, 4) H3K_CASE(4, 4) H3K_CASE(5, 4) H3K_CASE(6, 4)
@@ -393,7 +437,8 @@ static bool dispatch256(int npass, int wpr, const void* x, int64_t rows, int k, 
 static int check_rot_args(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int rot) {
   if (x_dtype != H3K_BF16 && x_dtype != H3K_F16 && x_dtype != H3K_F32)
     return fail(H3K_EINVAL, "activations must be bf16, f16 or f32 (dtype code %d)", x_dtype);
-  if (!is_pow4(rot)) return fail(H3K_EINVAL, "rotation block must be a power of 4 in [4, 1024], got %d", rot);
+  if (rot < 4 || rot > 1024 || (rot & (rot - 1)))
+    return fail(H3K_EINVAL, "rotation block must be a power of 2 in [4, 1024], got %d", rot);
   if (rows < 0 || k <= 0 || k % rot) return fail(H3K_EINVAL, "k=%lld must be a positive multiple of the rotation block %d", (long long)k, rot);
   if (k > (1 << 30)) return fail(H3K_EINVAL, "k=%lld too large", (long long)k);
   if (ldx < k) return fail(H3K_EINVAL, "ldx=%lld < k=%lld", (long long)ldx, (long long)k);
@@ -401,10 +446,10 @@ static int check_rot_args(const void* x, int x_dtype, int64_t rows, int64_t k, i
   return H3K_OK;
 }
 
-static int log4_of(int rot) {
+static int log2_of(int rot) {
   int l = 0;
   while (rot > 1) {
-    rot >>= 2;
+    rot >>= 1;
     ++l;
   }
   return l;
@@ -427,24 +472,27 @@ extern "C" int h3k_rotate_quant(const void* x, int x_dtype, int64_t rows, int64_
   const int es = x_dtype == H3K_F32 ? 4 : 2;
   int np = 0, wpr = 1;
   if (k <= (int64_t)256 * 128) rq_plan(static_cast<int>(k / 256), rows, np, wpr);
-  const bool fast = rot == 256 && x_dtype != H3K_F32 && aligned(x, 16) && (ldx * es) % 16 == 0 && aligned(q, 16) &&
-                    ldq % 16 == 0 && np > 0;
+  const bool fast = (rot == 256 || rot == 128) && x_dtype != H3K_F32 && aligned(x, 16) && (ldx * es) % 16 == 0 &&
+                    aligned(q, 16) && ldq % 16 == 0 && np > 0 && k % 256 == 0;
   if (fast) {
     const int kk = static_cast<int>(k);
     bool ok;
-    if (x_dtype == H3K_F16)
-      ok = eager ? dispatch256<true, true>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st)
-                 : dispatch256<true, false>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st);
-    else
-      ok = eager ? dispatch256<false, true>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st)
-                 : dispatch256<false, false>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st);
+#define H3K_RQ(F, E, R) dispatch256<F, E, kActNone, R>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st)
+    if (rot == 256) {
+      if (x_dtype == H3K_F16) ok = eager ? H3K_RQ(true, true, 256) : H3K_RQ(true, false, 256);
+      else ok = eager ? H3K_RQ(false, true, 256) : H3K_RQ(false, false, 256);
+    } else {
+      if (x_dtype == H3K_F16) ok = eager ? H3K_RQ(true, true, 128) : H3K_RQ(true, false, 128);
+      else ok = eager ? H3K_RQ(false, true, 128) : H3K_RQ(false, false, 128);
+    }
+#undef H3K_RQ
     if (!ok) return fail(H3K_EINVAL, "no fast rotation kernel for k=%lld", (long long)k);
     return check_launch("rotquant256");
   }
   const dim3 grid(static_cast<unsigned>(rows));
-  const int l4 = log4_of(rot), kk = static_cast<int>(k);
+  const int l2 = log2_of(rot), kk = static_cast<int>(k);
 #define H3K_GEN(DT, E) \
-  hipLaunchKernelGGL((rot_generic_kernel<DT, E, false>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4, q, ldq, xs, nullptr, 0)
+  hipLaunchKernelGGL((rot_generic_kernel<DT, E, false>), grid, dim3(256), 0, st, x, rows, kk, ldx, l2, q, ldq, xs, nullptr, 0)
   if (x_dtype == H3K_BF16) {
     if (eager) H3K_GEN(H3K_BF16, true); else H3K_GEN(H3K_BF16, false);
   } else if (x_dtype == H3K_F16) {
@@ -537,15 +585,15 @@ extern "C" int h3k_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, i
   if (!y) return fail(H3K_EINVAL, "y is NULL");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(rows));
-  const int l4 = log4_of(rot), kk = static_cast<int>(k);
+  const int l2 = log2_of(rot), kk = static_cast<int>(k);
   if (x_dtype == H3K_BF16)
-    hipLaunchKernelGGL((rot_generic_kernel<H3K_BF16, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4,
+    hipLaunchKernelGGL((rot_generic_kernel<H3K_BF16, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l2,
                        nullptr, 0, nullptr, y, ldy);
   else if (x_dtype == H3K_F16)
-    hipLaunchKernelGGL((rot_generic_kernel<H3K_F16, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4,
+    hipLaunchKernelGGL((rot_generic_kernel<H3K_F16, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l2,
                        nullptr, 0, nullptr, y, ldy);
   else
-    hipLaunchKernelGGL((rot_generic_kernel<H3K_F32, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l4,
+    hipLaunchKernelGGL((rot_generic_kernel<H3K_F32, false, true>), grid, dim3(256), 0, st, x, rows, kk, ldx, l2,
                        nullptr, 0, nullptr, y, ldy);
   return check_launch("rot_generic(rotate)");
 }

@@ -54,6 +54,29 @@ def hadamard_regular(size: int, device="cpu", dtype: torch.dtype = torch.float32
     return h
 
 
+def _check_rotation(size: int) -> None:
+    """Rotation sizes: the reference's powers of 4, plus the other powers of 2 in [8, 512] as an extension (H2 on
+    the top index bit, scale 1/sqrt(size) rounded once in fp64; see hadamard)."""
+    if size < 4 or size > 1024 or size & (size - 1):
+        raise ValueError(f"rotation block must be a power of 2 in [4, 1024] (the reference: a power of 4), got {size}")
+
+
+def hadamard(size: int, device="cpu", dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """The rotation matrix of any supported size: hadamard_regular for powers of 4; for the other powers of 2
+    (an extension the reference rejects) kron(H2, H4, ..., H4) / sqrt(size) with H2 = [[1, 1], [1, -1]] as the
+    most significant factor, built in fp64 and rounded once to `dtype`."""
+    _check_rotation(size)
+    if size & 0x155555:
+        return hadamard_regular(size, device, dtype)
+    h4 = torch.tensor(_H4, dtype=torch.float64)
+    full = torch.tensor(((1.0, 1.0), (1.0, -1.0)), dtype=torch.float64)
+    inner = h4
+    while inner.shape[0] * 2 < size:
+        inner = torch.kron(inner, h4)
+    full = torch.kron(full, inner) * (math.sqrt(2.0) * 2.0 ** -((size.bit_length()) // 2))
+    return full.to(device=device, dtype=dtype).contiguous()
+
+
 # --------------------------------------------------------------------------------------------- helpers
 def _need_gpu(t: torch.Tensor, what: str) -> None:
     if not t.is_cuda:
@@ -122,13 +145,13 @@ def rotate(x: torch.Tensor, size: int = CONVROT) -> torch.Tensor:
     k = x.shape[-1]
     if k % size:
         raise ValueError(f"last dim {k} is not a multiple of the rotation block {size}")
-    hadamard_regular(size)  # validates the size (power of 4)
+    _check_rotation(size)
     if x.numel() == 0:
         return x.clone()
     _need_gpu(x, "rotate")
     x2 = x.reshape(-1, k)
     if x.dtype == torch.float64:  # the reference's own fp64 path: one fp64 GEMM
-        y = torch.matmul(x2.reshape(-1, k // size, size), hadamard_regular(size, x.device, x.dtype)).reshape(-1, k)
+        y = torch.matmul(x2.reshape(-1, k // size, size), hadamard(size, x.device, x.dtype)).reshape(-1, k)
         return y.reshape(x.shape)
     x2 = _rows(x2)
     y = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
@@ -159,7 +182,7 @@ def quantize_activation(x: torch.Tensor, *, size: int = CONVROT, quant_mode: str
     k = x.shape[-1]
     if k % size:
         raise ValueError(f"last dim {k} is not a multiple of the rotation block {size}")
-    hadamard_regular(size)
+    _check_rotation(size)
     _need_gpu(x, "quantize_activation")
     q, s = _quantize_rows(x.reshape(math.prod(x.shape[:-1]), k), size, quant_mode)
     return q.reshape(x.shape), s.reshape(*x.shape[:-1], 1)
@@ -205,7 +228,7 @@ def dequantize(w: W4A8Weight, dtype: torch.dtype = torch.float32, rotated: bool 
     sub = W4A8Weight(w.q[r0:r1], w.s_rel[r0:r1], w.s_ch[r0:r1], w.codebook, w.group_size, w.convrot)
     wr = decode_int8_grid(sub).float().mul_(sub.s_ch.float().unsqueeze(1))
     if not rotated:
-        h = hadamard_regular(w.convrot, w.q.device, torch.float32)
+        h = hadamard(w.convrot, w.q.device, torch.float32)
         wr = torch.matmul(wr.view(max(r1 - r0, 0), k // w.convrot, w.convrot), h).view(max(r1 - r0, 0), k)
     return wr.to(dtype)
 

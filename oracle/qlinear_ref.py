@@ -8,7 +8,11 @@ against.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg m
 Pinning (what checks each function against something other than its own formula) lives in
 tests/test_oracle_*.py:
   hadamard_regular      closed form (kron of H4) + symmetric/involutory/dyadic entries + golden vectors
-  rotate_f32            brute-force rational arithmetic on tiny inputs + golden vectors
+  hadamard_pow2 / rotation_scale (sizes that are not powers of 4: an extension the reference rejects)
+                        an element-wise sign formula built independently of np.kron, orthogonality, the
+                        all-ones closed form that places H2 on the top bit, correctly rounded sqrt(2)
+  rotate_f32            brute-force rational arithmetic on tiny inputs + golden vectors; for the extension
+                        sizes, a digit-by-digit separable application of the factors
   quantize_rows         closed form KATs (degenerate rows), the division lemma, golden vectors of the
                         reference's own quantize_activation (tests/golden/)
   fp8_e4m3fn_to_f32     element-by-element OCP E4M3FN definition for all 256 bytes
@@ -92,18 +96,46 @@ def hadamard_regular(size: int) -> np.ndarray:
     return h / math.sqrt(size)
 
 
+_H2 = np.array([[1, 1], [1, -1]], dtype=np.float64)
+
+
+def hadamard_pow2(size: int) -> np.ndarray:
+    """Unnormalised +-1 Hadamard of a power-of-2 size in [4, 1024]: kron(H4, ..., H4) for powers of 4, else
+    kron(H2, H4, ..., H4) with H2 as the most significant factor.  Extension of the reference (which accepts powers
+    of 4 only): for a power of 4 it is hadamard_regular(size) * sqrt(size)."""
+    if size < 4 or size > 1024 or size & (size - 1):
+        raise ValueError(f"rotation size must be a power of 2 in [4, 1024], got {size}")
+    h = _H4
+    while h.shape[0] * 4 <= size:
+        h = np.kron(h, _H4)
+    return np.kron(_H2, h) if h.shape[0] < size else h
+
+
+def rotation_scale(size: int) -> float:
+    """1/sqrt(size) in fp64: exact for powers of 4; RN(sqrt(2)) * 2^-(log2(size) + 1) / 2 otherwise."""
+    bits = size.bit_length() - 1
+    if bits % 2 == 0:
+        return 2.0 ** -(bits // 2)
+    return math.sqrt(2.0) * 2.0 ** -((bits + 1) // 2)
+
+
 def rotate_f32(x: np.ndarray, size: int) -> np.ndarray:
     """[M, K] float values -> float32 [M, K]: block-wise x @ H accumulated in float64, rounded once.
 
-    Reference h3turbo/h3/qlinear.py:105-115 (`_rot32`, CPU branch: fp64 matmul then .float()).
+    Reference h3turbo/h3/qlinear.py:105-115 (`_rot32`, CPU branch: fp64 matmul then .float()).  Sizes that are not
+    powers of 4 (extension): the exact fp64 sum x @ hadamard_pow2(size), times rotation_scale(size) (one fp64
+    rounding), rounded to float32.
     """
     x = np.asarray(x)
     m, k = x.shape
     if k % size:
         raise ValueError(f"last dim {k} is not a multiple of the rotation block {size}")
-    h = hadamard_regular(size)
-    y = np.matmul(x.astype(np.float64).reshape(m, k // size, size), h).reshape(m, k)
-    return y.astype(np.float32)
+    blocks = x.astype(np.float64).reshape(m, k // size, size)
+    if size & 0x155555:  # a power of 4: the reference's normalised matrix
+        y = np.matmul(blocks, hadamard_regular(size))
+    else:
+        y = np.matmul(blocks, hadamard_pow2(size)) * rotation_scale(size)
+    return y.reshape(m, k).astype(np.float32)
 
 
 # ----------------------------------------------------------------------------------------- activation quantiser

@@ -32,9 +32,11 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     lib = _lib.load()
-    # rotation block not a power of 4
-    assert lib.h3k_rotate_quant(None, _lib.BF16, 4, 384, 384, 128, 0, None, 384, None, None) == _lib.EINVAL
-    assert "power of 4" in lib.h3k_last_error().decode()
+    # rotation block not a power of 2 (128 and the other powers of 2 are accepted: an extension of the reference)
+    assert lib.h3k_rotate_quant(None, _lib.BF16, 4, 384, 384, 48, 0, None, 384, None, None) == _lib.EINVAL
+    assert "power of 2" in lib.h3k_last_error().decode()
+    assert lib.h3k_rotate_quant(None, _lib.BF16, 0, 384, 384, 128, 0, None, 384, None, None) == 0  # no rows: no-op
+    assert lib.h3k_rotate_quant(None, _lib.BF16, 4, 384, 384, 2048, 0, None, 384, None, None) == _lib.EINVAL
     # k not a multiple of the block
     assert lib.h3k_rotate_quant(None, _lib.BF16, 4, 250, 250, 256, 0, None, 250, None, None) == _lib.EINVAL
     assert "multiple" in lib.h3k_last_error().decode()

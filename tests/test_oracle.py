@@ -266,3 +266,63 @@ def test_epilogue_orders_differ_in_fp32():
     xs = rng.random((64, 1)).astype(np.float32)
     sc = rng.random(64).astype(np.float32)
     assert not np.array_equal(ref.epilogue(acc, xs, sc, "f32", "ck"), ref.epilogue(acc, xs, sc, "f32", "eager"))
+
+
+# ------------------------------------------------------------------------------------------------ rotation extension
+# Sizes that are not powers of 4 (8, 32, 128, 512) are an extension: the reference rejects them.  These checks pin
+# the oracle's definition by means other than its own formula.
+EXT_SIZES = [8, 32, 128, 512]
+
+
+@pytest.mark.parametrize("size", EXT_SIZES)
+def test_pow2_hadamard_is_the_elementwise_sign_formula(size):
+    """H[i, j] = (-1)^(top bit of i and j) * prod over 2-bit digits d of H4[i_d, j_d], with H4[a, b] = -1 iff
+    a + b = 3: built by loops, independently of np.kron."""
+    bits = size.bit_length() - 1
+    want = np.ones((size, size))
+    for i in range(size):
+        for j in range(size):
+            sign = -1.0 if (i >> (bits - 1)) & (j >> (bits - 1)) & 1 else 1.0
+            for d in range((bits - 1) // 2):
+                if ((i >> (2 * d)) & 3) + ((j >> (2 * d)) & 3) == 3:
+                    sign = -sign
+            want[i, j] = sign
+    h = ref.hadamard_pow2(size)
+    assert np.array_equal(h, want)
+    assert np.array_equal(h @ h.T, size * np.eye(size)) and np.array_equal(h, h.T)
+
+
+@pytest.mark.parametrize("size", EXT_SIZES)
+def test_extension_scale_is_the_rounded_inverse_square_root(size):
+    c = ref.rotation_scale(size)
+    assert ref.rotation_scale(128) == float.fromhex("0x1.6a09e667f3bcdp-4")  # RN(sqrt 2) / 16
+    # c is fp64's nearest to 1/sqrt(size): c^2 * size lies within a few ulps of 1
+    assert abs(c * c * size - 1.0) < 4e-16
+
+
+@pytest.mark.parametrize("size", EXT_SIZES)
+def test_extension_rotation_of_ones_has_the_closed_form(size):
+    """All-ones rows: column sums of H are 2 per H4 digit and (2, 0) for the H2 top bit, so y_j = 2^((bits+1)/2) * c
+    where the top bit of j is 0 and 0 where it is 1: H2 sits on the top index bit, not the bottom one."""
+    bits = size.bit_length() - 1
+    y = ref.rotate_f32(np.ones((1, size), np.float32), size)
+    top = (np.arange(size) >> (bits - 1)) & 1
+    want = np.where(top == 0, np.float32(2.0 ** ((bits + 1) // 2) * ref.rotation_scale(size)), np.float32(0.0))
+    assert np.array_equal(y[0], want.astype(np.float32))
+
+
+@pytest.mark.parametrize("size", EXT_SIZES)
+def test_extension_rotation_equals_the_digit_by_digit_transform(size):
+    """The dense fp64 matmul against applying H2 on the top bit and H4 on each 2-bit digit separately (an FWHT):
+    exact integer sums, so the two orders agree bit for bit after the same scaling and rounding."""
+    bits = size.bit_length() - 1
+    rng = np.random.default_rng(size)
+    x = rng.integers(-1000, 1000, (3, 2 * size)).astype(np.float32) * np.float32(0.125)
+    v = x.astype(np.float64).reshape(3, 2, size)
+    axes = [2] + [4] * ((bits - 1) // 2)  # most significant first
+    v = v.reshape(3, 2, *axes)
+    v = np.moveaxis(np.tensordot(v, ref._H2, axes=([2], [0])), -1, 2)
+    for a in range(len(axes) - 1):
+        v = np.moveaxis(np.tensordot(v, ref._H4, axes=([3 + a], [0])), -1, 3 + a)
+    y = (v.reshape(3, 2 * size) * ref.rotation_scale(size)).astype(np.float32)
+    assert np.array_equal(ref.rotate_f32(x, size), y)
