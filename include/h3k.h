@@ -226,6 +226,16 @@ int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const 
                      void* stream);
 
 /*
+ * The DiT block's gated residual add, in place, bf16: x[t] += y[t] * gate[row_of_token[t]] per token row t, as one
+ * pass.  Replaces the per-segment x[a:b].addcmul_(y[a:b], gate[row].to(x.dtype)) of _gate_,
+ * h3turbo/h3/model.py:112-115.  gate is the gate already in bf16, one row of k per modulation row (stride ldg);
+ * row_of_token is int32 [rows].  Each element is bf16(fp32(x + y * gate)): the bf16 product is exact in fp32, so
+ * this equals torch's addcmul on bf16 tensors.  k a multiple of 8, rows and strides 16-byte aligned.
+ */
+int h3k_gated_add(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, int64_t ldg,
+                  const int32_t* row_of_token, int64_t rows, int64_t k, void* stream);
+
+/*
  * Host -> device copy of one weight block on the streaming engine's copy stream (hipMemcpyAsync).
  * Replaces the slot copy of h3turbo/h3/stream.py:346-354 (_issue: slot.buf.copy_(src, non_blocking)).
  * src is host memory (page-locked for an asynchronous copy), dst device memory.

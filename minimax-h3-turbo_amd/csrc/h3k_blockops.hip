@@ -70,9 +70,63 @@ __global__ __launch_bounds__(256) void rms_modulate_kernel(const uint16_t* __res
   }
 }
 
+// Gated residual add (reference h3turbo/h3/model.py:112-115, _gate_: x[tokens].addcmul_(y[tokens], gate[row].to(
+// x.dtype)), in place, bf16):
+//   x[t][e] = bf16(fp32(x[t][e]) + fp32(y[t][e]) * fp32(g[m][e]))    m = the token's modulation row
+// g is the gate already rounded to bf16.  The product of two bf16 values is exact in fp32, so this is one fp32
+// rounding of the sum (with or without an fma), then the rounding to bf16: torch's addcmul on bf16 tensors.
+// One thread per 8 elements (16-byte loads and stores); x and y are read once, x written once.
+__global__ __launch_bounds__(256) void gated_add_kernel(uint16_t* __restrict__ x, int64_t ldx,
+                                                        const uint16_t* __restrict__ y, int64_t ldy,
+                                                        const uint16_t* __restrict__ gate, int64_t ldg,
+                                                        const int32_t* __restrict__ row_of_token, int64_t rows,
+                                                        int chunks) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (u >= rows * chunks) return;
+  const int64_t t = u / chunks;
+  const int e0 = static_cast<int>(u - t * chunks) * 8;
+  const int64_t m = row_of_token[t];
+  u32x4* xp = reinterpret_cast<u32x4*>(x + t * ldx + e0);
+  const u32x4 xv = __builtin_nontemporal_load(xp);
+  const u32x4 yv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(y + t * ldy + e0));
+  const u32x4 gv = *reinterpret_cast<const u32x4*>(gate + m * ldg + e0);
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int sft = 16 * half;
+      const float xe = bf16_to_f32((xv[j] >> sft) & 0xFFFFu), ye = bf16_to_f32((yv[j] >> sft) & 0xFFFFu);
+      const float ge = bf16_to_f32((gv[j] >> sft) & 0xFFFFu);
+      word |= f32_to_bf16_bits(fp32_round_point(xe + fp32_round_point(ye * ge))) << sft;
+    }
+    o[j] = word;
+  }
+  __builtin_nontemporal_store(o, xp);
+}
+
 }  // namespace h3k
 
 using namespace h3k;
+
+extern "C" int h3k_gated_add(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, int64_t ldg,
+                             const int32_t* row_of_token, int64_t rows, int64_t k, void* stream) {
+  if (rows < 0 || k <= 0 || k % 8 || k > (int64_t(1) << 24))
+    return fail(H3K_EINVAL, "k=%lld must be a positive multiple of 8", (long long)k);
+  if (ldx < k || ldy < k || ldg < k) return fail(H3K_EINVAL, "row strides smaller than the rows");
+  if (rows == 0) return H3K_OK;
+  if (!x || !y || !gate || !row_of_token) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(x, 16) || !aligned(y, 16) || !aligned(gate, 16) || ldx % 8 || ldy % 8 || ldg % 8)
+    return fail(H3K_EINVAL, "rows must be 16-byte aligned (strides multiples of 8 elements)");
+  const int chunks = static_cast<int>(k / 8);
+  const int64_t threads = rows * chunks;
+  if ((threads + 255) / 256 > 0x7FFFFFFF) return fail(H3K_EINVAL, "too many elements for one launch");
+  hipLaunchKernelGGL(gated_add_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<uint16_t*>(x), ldx, static_cast<const uint16_t*>(y),
+                     ldy, static_cast<const uint16_t*>(gate), ldg, row_of_token, rows, chunks);
+  return check_launch("gated_add");
+}
 
 extern "C" int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const void* w, const void* shift,
                                 const void* scale, int64_t ldm, const int32_t* row_of_token, float eps, void* h,

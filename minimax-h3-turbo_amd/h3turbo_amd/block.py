@@ -124,10 +124,30 @@ def rms_modulate(x: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor, sca
     return h
 
 
-def gated_add_(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, segments: Sequence[Segment]) -> torch.Tensor:
-    """In place x[tokens] += y[tokens] * gate[row], one rounding (h3turbo/h3/model.py:112-115)."""
-    for a, b, row in _row_pieces(segments):
-        x[a:b].addcmul_(y[a:b], gate[row].to(x.dtype))
+def gated_add_(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, segments: Sequence[Segment],
+               rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """In place x[tokens] += y[tokens] * gate[row], one rounding (h3turbo/h3/model.py:112-115).  bf16 on the GPU with
+    every token covered by a segment: one HIP pass over x and y (h3k_gated_add) with the gate rows rounded to bf16
+    once, bit-identical to the per-segment addcmul_ (the bf16 product is exact in fp32); `rows` is
+    token_rows(segments) when already built."""
+    k = x.shape[-1]
+    fused = (x.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16 and x.dim() == 2 and y.dim() == 2
+             and k % 8 == 0 and gate.shape[-1] == k and x.stride(-1) == 1 and y.stride(-1) == 1
+             and x.data_ptr() % 16 == 0 and y.data_ptr() % 16 == 0
+             and (x.shape[0] <= 1 or (x.stride(0) % 8 == 0 and y.stride(0) % 8 == 0)))
+    if fused and rows is None:
+        rows = token_rows(segments, x.shape[0], x.device)
+    if not fused or rows is None:
+        for a, b, row in _row_pieces(segments):
+            x[a:b].addcmul_(y[a:b], gate[row].to(x.dtype))
+        return x
+    from . import _lib
+
+    g = gate.reshape(-1, k).to(torch.bfloat16).contiguous()
+    lib = _lib.load()
+    _lib.check(lib.h3k_gated_add(x.data_ptr(), x.stride(0) if x.shape[0] > 1 else k, y.data_ptr(),
+                                 y.stride(0) if y.shape[0] > 1 else k, g.data_ptr(), k, rows.data_ptr(), x.shape[0],
+                                 k, _lib.stream_of(x.device)), "h3k_gated_add")
     return x
 
 
@@ -356,9 +376,9 @@ class DiTBlock:
         eps = self.cfg.norm_eps
         rows = token_rows(segments, x.shape[0], x.device) if x.is_cuda else None
         h = rms_modulate(x, w.norm1, sh_a, sc_a, eps, segments, rows)
-        gated_add_(x, g_a, self.attention(h, w, rope), segments)
+        gated_add_(x, g_a, self.attention(h, w, rope), segments, rows)
         h = rms_modulate(x, w.norm2, sh_m, sc_m, eps, segments, rows)
-        return gated_add_(x, g_m, self.mlp(h, w), segments)
+        return gated_add_(x, g_m, self.mlp(h, w), segments, rows)
 
     __call__ = forward
 

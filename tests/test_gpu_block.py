@@ -320,3 +320,25 @@ def test_fused_rms_modulate_matches_the_torch_ops(s, k, int_valued):
         ulp = want.float().abs().clamp_min(1e-30) * 2.0 ** -7
         assert (diff <= ulp * 1.01 + 1e-30).all(), "more than one bf16 ulp away"
         assert (got != want).float().mean().item() < 0.01
+
+
+@pytest.mark.parametrize("s,k", [(37, 5120), (300, 1024), (1, 5376), (4099, 768)])
+def test_fused_gated_add_matches_the_torch_ops(s, k):
+    """h3k_gated_add (one pass) against the reference's per-segment x[a:b].addcmul_(y[a:b], gate[row].to(bf16)) on
+    the CPU (h3turbo/h3/model.py:112-115), bit for bit: scalar and per-token modulation rows, gates from fp32 AdaLN
+    rows as strided views, outputs and residuals over several magnitudes."""
+    print(f"gated_add s={s} k={k}", flush=True)
+    g = torch.Generator().manual_seed(s * 7 + k)
+    x = (torch.randn(s, k, generator=g) * torch.exp(2 * torch.randn(s, 1, generator=g))).to(torch.bfloat16)
+    y = (torch.randn(s, k, generator=g) * 3).to(torch.bfloat16)
+    z = torch.randn(3, 6 * k, generator=g) * 0.3  # fp32 modulation rows; the gate is a strided chunk of them
+    gate = z.view(3, -1).chunk(6, dim=-1)[2]
+    a, b = s // 3, 2 * s // 3
+    segments = [(0, a, 0), (a, b, torch.randint(0, 3, (b - a,), generator=g)), (b, s, 2)]
+    want = x.clone()
+    for p, q, r in segments:
+        want[p:q].addcmul_(y[p:q], gate[r].to(torch.bfloat16))
+    seg_gpu = [(p, q, r.to(DEV) if isinstance(r, torch.Tensor) else r) for p, q, r in segments]
+    xg = x.to(DEV)
+    out = bk.gated_add_(xg, gate.to(DEV), y.to(DEV), seg_gpu)
+    assert out is xg and torch.equal(xg.cpu(), want)
