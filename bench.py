@@ -474,10 +474,11 @@ def sweep_measurement(dev, steps: int):
     return rows
 
 
-def rotquant_config2(dev, steps: int = 20, rot: int = 256):
-    """rotate + quantise bf16 activations [12090, 5120] (1 % outlier channels x20), per-token
-    int8 output and fp32 scales; mean of `steps` launches (HIP events on the launch stream), HBM bytes = 2 MK
-    read + MK + 4 M written."""
+def rotquant_config2(dev, steps: int = 20, rot: int = 128):
+    """rotate + quantise bf16 activations [12090, 5120] (1 % outlier channels x20) with the
+    config's 128-wide block-Hadamard (an extension of the reference, which takes powers of 4), per-token int8 output
+    and fp32 scales; mean of `steps` launches (HIP events on the launch stream), HBM bytes = 2 MK read + MK + 4 M
+    written."""
     import torch
 
     from h3turbo_amd import _lib
@@ -622,9 +623,9 @@ def cpu_baseline(m: int, k: int, n: int, rows: int):
 
 def cpu_config1(threads: int, runs: int = 7):
     """BASELINE config 1 measured whole on the host: one W4A8 ConvRot QLinear, bf16 activations [256, 1024] with 1 %
-    outlier channels x20, int4 group-128 weight with fp16 scales [1024, 1024], seed 0, through the CPU oracle (weight
-    decode + rotate/quantise + exact int8 GEMM + epilogue); one warm-up, then the median of `runs` runs.  Rotation
-    256: the reference rejects the config's 128 (its Hadamard sizes are powers of 4)."""
+    outlier channels x20, int4 group-128 weight with fp16 scales [1024, 1024], seed 0, the config's rotation 128
+    (the oracle's extension of the reference), through the CPU oracle (weight decode + rotate/quantise + exact int8
+    GEMM + epilogue); one warm-up, then the median of `runs` runs."""
     import numpy as np
 
     import inputs as gi
@@ -636,7 +637,7 @@ def cpu_config1(threads: int, runs: int = 7):
 
     def once():
         w8 = ref.decode_int8_grid(q, s_rel, "f16", cb, 128)
-        xq, xs = ref.quantize_rows(x, "bf16", 256, "ck")
+        xq, xs = ref.quantize_rows(x, "bf16", 128, "ck")
         return ref.epilogue(ref.int8_mm_emulated(xq, w8), xs, s_ch, "bf16", "ck")
 
     once()
@@ -647,7 +648,7 @@ def cpu_config1(threads: int, runs: int = 7):
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     return {"ms": round(med * 1e3, 2), "TOPS": round(2.0 * m * n * k / med / 1e12, 6), "cores": int(threads),
-            "runs": runs, "sample": f"config 1 whole: M={m} K={k} N={n}, rotation 256, median of {runs} after 1 warm-up"}
+            "runs": runs, "sample": f"config 1 whole: M={m} K={k} N={n}, rotation 128, median of {runs} after 1 warm-up"}
 
 
 def main() -> None:
@@ -767,7 +768,8 @@ def main() -> None:
             "gemm_a8w8": {"ms": round(t_gemm, 4), "TOPS": round(gemm_tops, 1)},
         },
     }
-    line["kernels"]["rotate_quant_config2"] = rotquant_config2(dev)
+    line["kernels"]["rotate_quant_config2"] = rotquant_config2(dev, rot=128)
+    line["kernels"]["rotate_quant_config2_rot256"] = rotquant_config2(dev, rot=256)
     if not args.no_block:
         del xq, w8, out
         line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))

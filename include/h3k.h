@@ -226,6 +226,18 @@ int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const 
                      void* stream);
 
 /*
+ * W4A8 linear with unquantised activations ("a16"): out = round_out(fp32(y * s_ch) + bias), y = xr @ levels^T with
+ * fp32 accumulation, xr the rotated activation in bf16 or f16 (a_dtype), levels the decoded int8 grid [n, k]
+ * (h3k_decode_w4, row stride ldw).  Replaces _TorchRunner._a16's GEMM, h3turbo/h3/qlinear.py:407-424
+ * (torch.mm(xr, levels^T, out_dtype=fp32) on tensor cores, then * s_ch, + bias).  The levels are exact in the
+ * 16-bit dtype, so this is the 16-bit MFMA on (xr, levels).  bias is fp32 [n] or NULL.  k a multiple of 16; xr and
+ * level rows 16-byte aligned.
+ */
+int h3k_gemm_a16(const void* a, int a_dtype, int64_t lda, const int8_t* w8, int64_t ldw, const float* s_ch,
+                 const float* bias, int64_t m, int64_t n, int64_t k, void* out, int out_dtype, int64_t ldo,
+                 void* stream);
+
+/*
  * The DiT block's gated residual add, in place, bf16: x[t] += y[t] * gate[row_of_token[t]] per token row t, as one
  * pass.  Replaces the per-segment x[a:b].addcmul_(y[a:b], gate[row].to(x.dtype)) of _gate_,
  * h3turbo/h3/model.py:112-115.  gate is the gate already in bf16, one row of k per modulation row (stride ldg);

@@ -301,6 +301,8 @@ class _HipRunner:
         self.n, self.k = self.dw.n, self.dw.k
         self.ocode = _lib.act_code(out_dtype)
         self.bias = None if bias is None else bias.to(device=w.q.device, dtype=out_dtype).contiguous()
+        # a16 adds the bias in fp32 from its own dtype (qlinear.py:423), a8 after rounding it to out_dtype (:405)
+        self.bias32 = None if bias is None else bias.to(device=w.q.device, dtype=torch.float32).contiguous()
         self._w8: Optional[torch.Tensor] = None
         self._w8p: Optional[torch.Tensor] = None
         self.lib = _lib.load()
@@ -358,7 +360,7 @@ class _HipRunner:
                                               _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0),
                                               _lib.ptr(ws), None, _lib.stream_of(xq.device)), "h3k_gemm_w4a8")
             return
-        if (self.packed_ok and xs.data_ptr() % 16 == 0 and out.stride(0) >= self.n
+        if (self.packed_ok and xs.data_ptr() % 16 == 0 and out.stride(0) >= self.n and m * self.k < (1 << 32)
                 and self.lib.h3k_gemm_packed_serves(m, self.n, self.k)):
             _lib.check(self.lib.h3k_gemm_a8w8_packed(xq.data_ptr(), self.k, xs.data_ptr(), self.w8p.data_ptr(),
                                                      self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
@@ -372,12 +374,22 @@ class _HipRunner:
 
     def _a16(self, x2: torch.Tensor, out: torch.Tensor) -> None:
         """Unquantised activation (qlinear.py:407-424): rotated x (rounded to x.dtype) times the exact int8 levels
-        with fp32 accumulation, s_ch applied to the fp32 result, rounded once."""
-        xr = rotate(x2, self.w.convrot).to(torch.float32)
-        y = torch.mm(xr, self.w8.to(torch.float32).t())
+        with fp32 accumulation, s_ch applied to the fp32 result, rounded once.  bf16 / f16 activations run on the
+        16-bit MFMA GEMM h3k_gemm_a16 (the levels widened exactly); fp32 ones (the reference's plain fp32 GEMM) on
+        torch.mm in fp32."""
+        xr = rotate(x2, self.w.convrot)
+        if xr.dtype in (torch.bfloat16, torch.float16):
+            xr = _rows(xr)
+            w8 = self.w8
+            _lib.check(self.lib.h3k_gemm_a16(xr.data_ptr(), _lib.act_code(xr.dtype), _ld(xr), w8.data_ptr(), self.k,
+                                             self.dw.s_ch.data_ptr(), _lib.ptr(self.bias32), xr.shape[0], self.n, self.k,
+                                             out.data_ptr(), self.ocode, out.stride(0) if out.shape[0] > 1 else self.n,
+                                             _lib.stream_of(xr.device)), "h3k_gemm_a16")
+            return
+        y = torch.mm(xr.to(torch.float32), self.w8.to(torch.float32).t())
         y.mul_(self.dw.s_ch)
-        if self.bias is not None:
-            y.add_(self.bias.to(torch.float32))
+        if self.bias32 is not None:
+            y.add_(self.bias32)
         out.copy_(y)
 
 

@@ -261,6 +261,26 @@ def linear_a8(x: np.ndarray, x_dtype: str, q: np.ndarray, s_rel: np.ndarray, s_k
     return epilogue(acc, xs, s_ch, out_dtype, mode, bias), xq, xs, acc
 
 
+def linear_a16(x: np.ndarray, x_dtype: str, q: np.ndarray, s_rel: np.ndarray, s_kind: str, s_ch: np.ndarray,
+               codebook: np.ndarray, group: int, convrot: int, *, out_dtype: Optional[str] = None,
+               bias: Optional[np.ndarray] = None):
+    """W4A8 linear with unquantised activations.  Reference h3turbo/h3/qlinear.py:407-424 (`_TorchRunner._a16`):
+    xr = rotate(x) rounded to x's dtype; y = xr @ levels^T accumulated in fp32 (tensor cores, any order); y *= s_ch;
+    y += bias (fp32); rounded once to out_dtype.  The oracle takes the exact sum (fp64 of bf16/f16 values times int8
+    levels), rounds it once to fp32, then applies s_ch and bias in fp32: the fp32-accumulated result of any summation
+    order lies within K * 2^-24 * sum|xr * level| of that sum.  Returns (out float32 holding out_dtype values, y_exact
+    fp64, abs_sum fp64) so a test can bound the accumulation error."""
+    out_dtype = out_dtype or x_dtype
+    xr = round_to(rotate_f32(x, convrot), x_dtype).astype(np.float64)
+    w8 = decode_int8_grid(q, s_rel, s_kind, codebook, group).astype(np.float64)
+    y_exact = xr @ w8.T
+    abs_sum = np.abs(xr) @ np.abs(w8).T
+    y = (y_exact.astype(np.float32) * np.asarray(s_ch, np.float32)[None, :]).astype(np.float32)
+    if bias is not None:
+        y = (y + np.asarray(bias, np.float32)[None, :]).astype(np.float32)
+    return round_to(y, out_dtype), y_exact, abs_sum
+
+
 # ----------------------------------------------------------------------------------------- swiglu / gelu
 def swiglu_bf16(h: np.ndarray) -> np.ndarray:
     """silu(gate) * up on [gate | up] halves, each op rounded to bf16 (qlinear.py:376-379)."""
