@@ -24,6 +24,30 @@
 
 namespace h3k {
 
+typedef __attribute__((address_space(3))) const uint16_t* lds_u16p;
+
+// h[r][31:16] = the 16-bit LDS value at src + 32 r bytes, h[r][15:0] kept, r = 0..15; the loads and their wait are
+// one statement, so no use of h can be scheduled before the data has arrived.
+__device__ __forceinline__ void load16_d16_hi(uint32_t (&h)[16], lds_u16p src) {
+  __asm__ volatile(
+      "ds_read_u16_d16_hi %0, %16\n\tds_read_u16_d16_hi %1, %16 offset:32\n\t"
+      "ds_read_u16_d16_hi %2, %16 offset:64\n\tds_read_u16_d16_hi %3, %16 offset:96\n\t"
+      "ds_read_u16_d16_hi %4, %16 offset:128\n\tds_read_u16_d16_hi %5, %16 offset:160\n\t"
+      "ds_read_u16_d16_hi %6, %16 offset:192\n\tds_read_u16_d16_hi %7, %16 offset:224\n\t"
+      "ds_read_u16_d16_hi %8, %16 offset:256\n\tds_read_u16_d16_hi %9, %16 offset:288\n\t"
+      "ds_read_u16_d16_hi %10, %16 offset:320\n\tds_read_u16_d16_hi %11, %16 offset:352\n\t"
+      "ds_read_u16_d16_hi %12, %16 offset:384\n\tds_read_u16_d16_hi %13, %16 offset:416\n\t"
+      "ds_read_u16_d16_hi %14, %16 offset:448\n\tds_read_u16_d16_hi %15, %16 offset:480\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "+v"(h[0]), "+v"(h[1]), "+v"(h[2]), "+v"(h[3]), "+v"(h[4]), "+v"(h[5]), "+v"(h[6]), "+v"(h[7]), "+v"(h[8]),
+        "+v"(h[9]), "+v"(h[10]), "+v"(h[11]), "+v"(h[12]), "+v"(h[13]), "+v"(h[14]), "+v"(h[15])
+      : "v"(src)
+      : "memory");
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 // y = x @ H4 on four values (H4 symmetric): (s - 2d, s - 2c, s - 2b, s - 2a) with s = a + b + c + d.
 __device__ __forceinline__ void h4(double& a, double& b, double& c, double& d) {
   const double s = (a + b) + (c + d);
@@ -46,16 +70,6 @@ constexpr double kSqrt2 = 0x1.6a09e667f3bcdp+0;  // RN(sqrt(2))
 // 1/sqrt(2^log2) in fp64: exact for even log2, RN(sqrt 2) * 2^-(log2 + 1) / 2 for odd log2.
 __device__ __forceinline__ double rot_scale(int log2) {
   return (log2 & 1) ? kSqrt2 * ldexp(1.0, -(log2 + 1) / 2) : ldexp(1.0, -log2 / 2);
-}
-
-// Same, folding the final 1/16 of H256 in: every operation stays exact (power-of-two scaling).
-__device__ __forceinline__ void h4_div16(double& a, double& b, double& c, double& d) {
-  const double s = ((a + b) + (c + d)) * 0.0625;
-  const double na = fma(d, -0.125, s), nb = fma(c, -0.125, s), nc = fma(b, -0.125, s), nd = fma(a, -0.125, s);
-  a = na;
-  b = nb;
-  c = nc;
-  d = nd;
 }
 
 template <bool F16>
@@ -170,6 +184,7 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
   uint16_t* tin = reinterpret_cast<uint16_t*>(&s_mid[wave][g * kMidStride]);
   double* tmid = &s_mid[wave][g * kMidStride];
   uint32_t yb[NPASS][8];  // rounded rotation, two 16-bit values per word, contiguous elements l*16 ..
+  uint32_t hv[16] = {};   // bf16 input words (value in the high half, zero low half)
   float amax = 0.0f;
 
 #pragma unroll
@@ -180,9 +195,21 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     *reinterpret_cast<u32x4*>(tin + l * 16) = raw[p][0];
     *reinterpret_cast<u32x4*>(tin + l * 16 + 8) = raw[p][1];
     wave_lds_sync();
+    // The 1/16 of H256 (or of 1/sqrt(128) = sqrt(2)/16) is applied here, to the fp32 inputs: a power-of-two
+    // scaling, exact for every bf16 and f16 value (the smallest, 2^-133 and 2^-24, stay fp32-representable), so
+    // every partial sum below is the exact sum of the scaled terms and the transforms need no scale step.
     double v[16];
+    if constexpr (!F16) {
+      // bf16 -> fp32 is the bf16 bits in the high half of a word whose low half is zero: ds_read_u16_d16_hi loads
+      // them there and keeps the low half, which these registers only ever hold as zero (no shift per element).
+      const lds_u16p src = (lds_u16p)(tin + l);
+      load16_d16_hi(hv, src);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = static_cast<double>(to_f32_16<F16>(tin[r * 16 + l]));
+      for (int r = 0; r < 16; ++r) v[r] = static_cast<double>(__uint_as_float(hv[r]) * 0.0625f);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = static_cast<double>(to_f32_16<F16>(tin[r * 16 + l]) * 0.0625f);
+    }
     // (2) digit 2 (r = d2 + 4*d3) and digit 3
 #pragma unroll
     for (int d3 = 0; d3 < 4; ++d3) h4(v[4 * d3], v[4 * d3 + 1], v[4 * d3 + 2], v[4 * d3 + 3]);
@@ -204,29 +231,31 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
     double w[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) w[j] = tmid[l * kMidRow + j];
-    // (4) digit 0 (j = d0 + 4*d1), then digit 1 with the 1/16 folded in
+    // (4) digit 0 (j = d0 + 4*d1), then digit 1
 #pragma unroll
     for (int d1 = 0; d1 < 4; ++d1) h4(w[4 * d1], w[4 * d1 + 1], w[4 * d1 + 2], w[4 * d1 + 3]);
-    if constexpr (ROT == 256) {
 #pragma unroll
-      for (int d0 = 0; d0 < 4; ++d0) h4_div16(w[d0], w[d0 + 4], w[d0 + 8], w[d0 + 12]);
-    } else {  // exact sums, then the one fp64 rounding of the 1/sqrt(128) scale
+    for (int d0 = 0; d0 < 4; ++d0) h4(w[d0], w[d0 + 4], w[d0 + 8], w[d0 + 12]);
+    if constexpr (ROT == 128) {  // exact sums of the scaled terms, then the one fp64 rounding of the sqrt(2) factor
 #pragma unroll
-      for (int d0 = 0; d0 < 4; ++d0) h4(w[d0], w[d0 + 4], w[d0 + 8], w[d0 + 12]);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) w[j] *= kSqrt2 * 0.0625;
+      for (int j = 0; j < 16; ++j) w[j] *= kSqrt2;
     }
     // (5) one rounding to fp32, absmax, one rounding to the activation dtype
 #pragma unroll
     for (int j = 0; j < 16; j += 2) {
       const float y0 = static_cast<float>(w[j]), y1 = static_cast<float>(w[j + 1]);
-      const uint32_t b0 = round_bits_16<F16>(y0), b1 = round_bits_16<F16>(y1);
+      uint32_t pair;
+      if constexpr (F16) {
+        pair = round_bits_16<F16>(y0) | (round_bits_16<F16>(y1) << 16);
+      } else {  // one RNE conversion for the pair
+        pair = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){y0, y1}, bf16x2));
+      }
       if (EAGER) {
-        amax = nan_max(amax, nan_max(fabsf(to_f32_16<F16>(b0)), fabsf(to_f32_16<F16>(b1))));
+        amax = nan_max(amax, nan_max(fabsf(to_f32_16<F16>(pair & 0xFFFFu)), fabsf(to_f32_16<F16>(pair >> 16))));
       } else {
         amax = nan_max(amax, nan_max(fabsf(y0), fabsf(y1)));
       }
-      yb[p][j >> 1] = b0 | (b1 << 16);
+      yb[p][j >> 1] = pair;
     }
   }
 
@@ -294,8 +323,6 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
         const uint32_t wv = yb[p][h];
         const float t0 = fp32_round_point(__uint_as_float(wv << 16) * rs);
         const float t1 = fp32_round_point(__uint_as_float(wv & 0xFFFF0000u) * rs);
-        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
         const uint32_t tb = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){t0, t1}, bf16x2));
         const float r0 = __builtin_amdgcn_fmed3f(__uint_as_float(tb << 16), -128.0f, 127.0f);
         const float r1 = __builtin_amdgcn_fmed3f(__uint_as_float(tb & 0xFFFF0000u), -128.0f, 127.0f);
