@@ -105,8 +105,9 @@ int h3k_decode_w4_packed(const void* q, int64_t ldq, const void* s_rel, int s_dt
  * counterpart: for callers holding a decoded grid. */
 int h3k_pack_w8(const int8_t* w8, int64_t ldw, int64_t n, int64_t k, int8_t* w8p, void* stream);
 
-/* 1 when h3k_gemm_a8w8_packed serves an m x n x k GEMM (k a multiple of 256, at least 512; enough 256 x 256 output
- * tiles to fill the chip), else 0. */
+/* 1 when h3k_gemm_a8w8_packed serves an m x n x k GEMM (k a multiple of 256, at least 512; more than 512 rows and
+ * enough 256 x 256 output tiles to fill the chip, and by the launch's cost model no slower than the row-major
+ * pipeline), else 0: the route the W4A8 linear takes. */
 int h3k_gemm_packed_serves(int64_t m, int64_t n, int64_t k);
 
 /*
@@ -119,6 +120,25 @@ int h3k_gemm_packed_serves(int64_t m, int64_t n, int64_t k);
 int h3k_gemm_a8w8_packed(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
                          const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out, int out_dtype,
                          int64_t ldo, int32_t* acc_out, void* stream);
+
+/*
+ * Bytes of the split-tail workspace h3k_gemm_a8w8_packed_ws uses for an m x n x k GEMM, 0 when it runs whole tiles
+ * only.  The split: when the last round of 256 x 256 tiles would leave CUs idle and the cost model of the launch says
+ * it pays, those tiles are cut along K into pieces (one per idle CU) whose int32 partial sums a fix-up kernel adds
+ * (exact) before the epilogue.
+ */
+int64_t h3k_gemm_packed_split_bytes(int64_t m, int64_t n, int64_t k);
+
+/*
+ * h3k_gemm_a8w8_packed without the accumulator dump, for any shape the packed kernel runs (k a multiple of 256, at
+ * least 512, m >= 4, n a multiple of 4), taking the split tail for 16-bit outputs when the workspace holds
+ * h3k_gemm_packed_split_bytes(m, n, k) bytes (256-byte aligned); with a smaller workspace (or none), whole tiles.
+ * Results are bit-identical either way.
+ * Replaces h3turbo/h3/qlinear.py:236-254 (_int8_mm) and :396-405 (_TorchRunner._a8 epilogue).
+ */
+int h3k_gemm_a8w8_packed_ws(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
+                            const void* bias, int64_t m, int64_t n, int64_t k, int mode, void* out, int out_dtype,
+                            int64_t ldo, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * W4A8 GEMM for few token rows (m <= 128): the int4 weight is decoded in registers into the int8 MFMA operands,
@@ -143,7 +163,9 @@ int h3k_gemm_w4a8(const int8_t* a, int64_t lda, const float* xs, const void* q, 
  * of 64: the fused few-row GEMM, no decode pass; shapes h3k_gemm_packed_serves accepts: the packed grid and its
  * GEMM; otherwise the row-major grid and h3k_gemm_a8w8.
  * Fills the slot of comfy_kitchen's w4a8_int8_linear call, h3turbo/h3/qlinear.py:427-429 (_run_ck).
- * workspace: device scratch of at least h3k_w4a8_linear_workspace(m, n, k) bytes, 256-byte aligned.
+ * workspace: device scratch of h3k_w4a8_linear_workspace(m, n, k) bytes, 256-byte aligned.  That size includes
+ * the packed GEMM's split tail where it is taken; a workspace without it (the activations, their scales and the
+ * weight grid only) is accepted and runs whole tiles.
  */
 size_t h3k_w4a8_linear_workspace(int64_t m, int64_t n, int64_t k);
 int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* q, int64_t ldq,

@@ -38,15 +38,17 @@ static inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; 
 
 int64_t w8p_bytes(int64_t n, int64_t k);
 bool w8p_serves(int64_t m, int64_t n, int64_t k);
+int64_t w8p_split_bytes(int64_t m, int64_t n, int64_t k);
+size_t w4a8_linear_base_workspace(int64_t m, int64_t n, int64_t k);
 void gemm_w8p_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
                      const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo, int32_t* acc_out,
-                     hipStream_t st);
+                     int32_t* part, hipStream_t st);
 
 }  // namespace h3k
 
 using namespace h3k;
 
-extern "C" int h3k_version(void) { return 4; }
+extern "C" int h3k_version(void) { return 5; }
 
 extern "C" const char* h3k_last_error(void) { return g_last_error.c_str(); }
 
@@ -75,10 +77,21 @@ static bool fused_few_rows(int64_t m, int64_t k, int group, const void* q, int64
          aligned(q, 16) && ldq % 16 == 0;
 }
 
-extern "C" size_t h3k_w4a8_linear_workspace(int64_t m, int64_t n, int64_t k) {
+// Activations, their scales and the weight region: what every call needs.
+size_t h3k::w4a8_linear_base_workspace(int64_t m, int64_t n, int64_t k) {
   if (m < 0 || n < 0 || k < 0) return 0;
   return round_up(static_cast<size_t>(m) * k, 256) + round_up(static_cast<size_t>(m) * 4, 256) +
          round_up(weight_region(m, n, k), 256);
+}
+
+// The packed GEMM's split-tail partial sums, for the shapes whose route takes it (the caller checks the rest).
+static size_t split_region(int64_t m, int64_t n, int64_t k) {
+  return m > kFewRows && w8p_serves(m, n, k) ? round_up(static_cast<size_t>(w8p_split_bytes(m, n, k)), 256) : 0;
+}
+
+extern "C" size_t h3k_w4a8_linear_workspace(int64_t m, int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k < 0) return 0;
+  return w4a8_linear_base_workspace(m, n, k) + split_region(m, n, k);
 }
 
 extern "C" int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* q,
@@ -86,7 +99,7 @@ extern "C" int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k,
                                const float* codebook, int64_t n, int group, int rot, const void* bias, int mode,
                                void* out, int out_dtype, int64_t ldo, void* workspace, size_t workspace_bytes,
                                void* stream) {
-  const size_t need = h3k_w4a8_linear_workspace(m, n, k);
+  const size_t need = w4a8_linear_base_workspace(m, n, k);
   if (workspace_bytes < need)
     return fail(H3K_ESPACE, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
   if (m == 0 || n == 0) return H3K_OK;
@@ -105,8 +118,10 @@ extern "C" int h3k_w4a8_linear(const void* x, int x_dtype, int64_t m, int64_t k,
       (out_dtype == H3K_BF16 || out_dtype == H3K_F16 || out_dtype == H3K_F32) && out) {
     rc = h3k_decode_w4_packed(q, ldq, s_rel, s_dtype, lds, codebook, n, k, group, w8, stream);
     if (rc) return rc;
+    const size_t split = split_region(m, n, k);  // taken when the workspace holds it
+    int32_t* part = split > 0 && workspace_bytes >= need + split ? reinterpret_cast<int32_t*>(ws + need) : nullptr;
     gemm_w8p_launch(aq, k, xs, w8, s_ch, bias, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), mode, out,
-                    out_dtype, ldo, nullptr, static_cast<hipStream_t>(stream));
+                    out_dtype, ldo, nullptr, part, static_cast<hipStream_t>(stream));
     return check_launch("gemm_a8w8_packed");
   }
   rc = h3k_decode_w4(q, ldq, s_rel, s_dtype, lds, codebook, n, k, group, w8, k, stream);

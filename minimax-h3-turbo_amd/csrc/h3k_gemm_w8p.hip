@@ -88,7 +88,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
                                                           int M, int N, int K, const float* __restrict__ xs,
                                                           const float* __restrict__ sch, const void* __restrict__ bias,
                                                           void* __restrict__ out, int64_t ldo,
-                                                          int32_t* __restrict__ acc_out, bool vec_out) {
+                                                          int32_t* __restrict__ acc_out, bool vec_out, int tiles_dp,
+                                                          int P, int KP, int32_t* __restrict__ part) {
   constexpr int WMB = 4, WNB = 4;   // a wavefront's 4 x 4 blocks of 32 x 32
   constexpr int BM = 256, BN = 256;
   constexpr int STAGE = BM * kBK;   // 16 KiB of activations per K-step
@@ -113,16 +114,32 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
 
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int tiles = tiles_m * tiles_n;
-  const int T = (tiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
-  const int KT = K / kBK;  // a multiple of S, >= 2 * S (host)
+  const int NG = static_cast<int>(gridDim.x), bid = static_cast<int>(blockIdx.x);
+  // Items of this workgroup: the whole tiles bid, bid + NG, ... below tiles_dp, then (split tail, 16-bit outputs
+  // only) piece bid of the tiles from tiles_dp on: tail tile bid / P, K-steps [(bid % P) KP, (bid % P + 1) KP),
+  // whose int32 partial sums go to part[bid] for w8p_fixup_kernel.
+  const int T_dp = bid < tiles_dp ? (tiles_dp - bid + NG - 1) / NG : 0;
+  const bool piece = FAST && P > 1 && bid < (tiles - tiles_dp) * P;
+  const int T = T_dp + (piece ? 1 : 0);
+  if (T == 0) return;  // the whole workgroup: nothing was issued yet
+  const int KT = K / kBK;  // a multiple of S, >= 2 * S (host); KP likewise
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int kh = lane >> 5;
 
-  auto coords = [&](int it, int& m0, int& n0) {
+  // item it -> tile origin, first K-step and K-step count
+  auto coords = [&](int it, int& m0, int& n0, int& k0, int& kt) {
+    int t = bid + it * NG;
+    k0 = 0;
+    kt = KT;
+    if (FAST && it >= T_dp) {
+      t = tiles_dp + bid / P;
+      k0 = (bid % P) * KP;
+      kt = KP;
+    }
     int tm, tn;
-    tile_coords<H3K_PIPE_GM>(static_cast<int>(blockIdx.x) + it * static_cast<int>(gridDim.x), tiles_m, tiles_n, tm, tn);
+    tile_coords<H3K_PIPE_GM>(t, tiles_m, tiles_n, tm, tn);
     m0 = tm * BM;
     n0 = tn * BN;
   };
@@ -140,7 +157,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   uint32_t astep = 0;   // activations: K position of the next stage to load, in bytes
   uint32_t bnext = 0;   // weights: offset of this wavefront's 4 blocks at the next K-step to load
   uint32_t bfirst = 0;  // ... and at K-step 0 of the tile being loaded (a safe address for the tail loads)
-  auto point_loads = [&](int m0, int n0) {
+  auto point_loads = [&](int m0, int n0, int k0) {
     // recomputed from an opaque lane index each time: kept from the prologue, these would be spilled
     int l = static_cast<int>(threadIdx.x & 63);
     __asm__ volatile("" : "+v"(l));
@@ -150,8 +167,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
                 static_cast<uint32_t>(swz_chunk(r, l & 3) * 16);
     });
     bfirst = static_cast<uint32_t>((n0 >> 5) + wn * WNB) * kBlockBytes;
-    bnext = bfirst;
-    astep = 0;
+    bnext = FAST ? bfirst + static_cast<uint32_t>(k0) * bstride : bfirst;
+    astep = FAST ? static_cast<uint32_t>(k0) * kBK : 0u;
   };
   // Waves 0, 1 and 2 load the tile's 256 xs, 256 s_ch and 256 bias values, one 16-byte chunk per lane.  A chunk
   // past the end of its array is clamped to the 16-byte chunk that holds the last element (the arrays are 16-byte
@@ -425,9 +442,43 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     }
   };
 
+  // A piece's int32 partial sums, row-major [256][256] at part[bid], through the staging area: each lane reads 8
+  // consecutive columns of a row back, so the 16 lanes of a row store its 128 columns of this wavefront as 512
+  // contiguous bytes.
+  auto dump_partial = [&]() {
+    if constexpr (FAST) {
+      int lane = static_cast<int>(threadIdx.x & 63);
+      __asm__ volatile("" : "+v"(lane));
+      const int kh = lane >> 5;
+      int32_t* const stg = reinterpret_cast<int32_t*>(smem + S * STAGE + RS * SLOT * 4) + wave * (32 * GROW);
+      int32_t* const dst = part + static_cast<int64_t>(bid) * (BM * BN);
+      static_for<WMB>([&](auto i) {
+        __builtin_amdgcn_sched_barrier(0);
+        int32_t* const w = stg + (lane & 31) * GROW + kh * 4;
+        static_for<WNB>([&](auto j) {
+          static_for<4>([&](auto g) {
+            *reinterpret_cast<v4i*>(w + j * 32 + g * 8) =
+                v4i{acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]};
+          });
+        });
+        wave_lds_sync();
+        const int32_t* const rp = stg + (lane >> 4) * GROW + (lane & 15) * 8;
+        static_for<8>([&](auto q) {
+          const v4i lo = *reinterpret_cast<const v4i*>(rp + q * 4 * GROW);
+          const v4i hi = *reinterpret_cast<const v4i*>(rp + q * 4 * GROW + 4);
+          int32_t* const o = dst + (wm * 128 + i * 32 + q * 4 + (lane >> 4)) * BN + wn * 128 + (lane & 15) * 8;
+          *reinterpret_cast<v4i*>(o) = lo;
+          *reinterpret_cast<v4i*>(o + 4) = hi;
+        });
+        wave_lds_sync();  // the next block overwrites the staging area
+      });
+    }
+  };
+
   // ---------------------------------------------------------------- prologue
-  coords(0, cm0, cn0);
-  point_loads(cm0, cn0);
+  int ck0 = 0, ckt = KT;  // the current item's first K-step and K-step count
+  coords(0, cm0, cn0, ck0, ckt);
+  point_loads(cm0, cn0, ck0);
   load_scales(0, cm0, cn0);
   static_for<S>([&](auto s) {
     issue_a(s, true);
@@ -492,13 +543,13 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   using std::integral_constant;
   for (; it < T; ++it) {
     has_next = it + 1 < T;
-    int nm0 = 0, nn0 = 0;  // the next tile's origin
-    if (has_next) coords(it + 1, nm0, nn0);
+    int nm0 = 0, nn0 = 0, nk0 = 0, nkt = KT;  // the next item
+    if (has_next) coords(it + 1, nm0, nn0, nk0, nkt);
     if (it > 0) {
       if constexpr (CROSS) {
         load_scales(it % RS, cm0, cn0);
       } else {
-        point_loads(cm0, cn0);
+        point_loads(cm0, cn0, ck0);
         load_scales(it % RS, cm0, cn0);
         static_for<S>([&](auto s) {
           issue_a(s, true);
@@ -513,21 +564,27 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
       constexpr int U = decltype(u)::value;
       step(u, integral_constant<bool, U == 0>{}, integral_constant<int, U < S - 1 ? W_AFTER_EPI : W_STEADY>{}, true, true);
     });
-    for (int kt0 = S; kt0 < KT - S; kt0 += S) {
+    for (int kt0 = S; kt0 < (FAST ? ckt : KT) - S; kt0 += S) {
       static_for<S>([&](auto u) {
         step(u, integral_constant<bool, false>{}, integral_constant<int, W_STEADY>{}, true, true);
       });
     }
-    if (CROSS && has_next) point_loads(nm0, nn0);  // the load streams move on to the next tile
+    if (CROSS && has_next) point_loads(nm0, nn0, nk0);  // the load streams move on to the next item
     static_for<S>([&](auto u) {  // steps KT - S .. KT - 1
       step(u, integral_constant<bool, false>{}, integral_constant<int, CROSS ? W_TAIL : W_DRAIN>{}, has_next,
            decltype(u)::value < S - 1);
     });
-    exact = epilogue(it % RS);
+    if (piece && it == T - 1) {
+      dump_partial();  // the last item: nothing is in flight behind it
+    } else {
+      exact = epilogue(it % RS);
+    }
     if (has_next) {
       if constexpr (CROSS) read_frags(0, 0, a0);
       cm0 = nm0;
       cn0 = nn0;
+      ck0 = nk0;
+      ckt = nkt;
     }
   }
   wait_vmcnt<0>();  // no direct-to-LDS write may land after the workgroup has ended
@@ -537,14 +594,80 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
 #define H3K_W8P_S 4
 #endif
 
+// Split tail: the int32 partial sums of the P pieces of each tail tile added in a fixed order (exact), then the
+// kernel's 16-bit epilogue.  One workgroup per 16 rows of a tail tile; a thread owns 16 consecutive columns of a row,
+// so a row's 256 partial sums are 1 KiB contiguous per piece.
+template <int ODT, bool EAGER>
+__global__ __launch_bounds__(256) void w8p_fixup_kernel(const int32_t* __restrict__ part, int P, int tiles_dp, int M,
+                                                        int N, const float* __restrict__ xs,
+                                                        const float* __restrict__ sch, const void* __restrict__ bias,
+                                                        uint16_t* __restrict__ out, int64_t ldo, bool vec_out) {
+  constexpr int BM = 256, BN = 256;
+  const int tt = static_cast<int>(blockIdx.x) >> 4, rg = static_cast<int>(blockIdx.x) & 15;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords<H3K_PIPE_GM>(tiles_dp + tt, tiles_m, tiles_n, tm, tn);
+  const int r = rg * 16 + static_cast<int>(threadIdx.x >> 4), c = static_cast<int>(threadIdx.x & 15) * 16;
+  const int m = tm * BM + r, n0 = tn * BN + c;
+  if (m >= M || n0 >= N) return;
+  int a[16];
+  for (int e = 0; e < 16; ++e) a[e] = 0;
+  for (int p = 0; p < P; ++p) {
+    const v4i* src = reinterpret_cast<const v4i*>(part + (static_cast<int64_t>(tt) * P + p) * (BM * BN) + r * BN + c);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const v4i x = __builtin_nontemporal_load(src + v);
+      a[4 * v] += x[0];
+      a[4 * v + 1] += x[1];
+      a[4 * v + 2] += x[2];
+      a[4 * v + 3] += x[3];
+    }
+  }
+  const float x = xs[m];
+  uint32_t bits[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int n = min(n0 + e, N - 1);  // columns past N are computed on the last one and never stored
+    const float sc = sch[n];
+    float y = EAGER ? value_point(static_cast<float>(a[e]) * value_point(x * sc))
+                    : value_point(value_point(static_cast<float>(a[e]) * x) * sc);
+    if (bias) {  // added after the output rounding (qlinear.py:404-405)
+      const uint32_t b = static_cast<const uint16_t*>(bias)[n];
+      const float rb = ODT == H3K_F16 ? round_f16(y) : round_bf16(y);
+      y = value_point(rb + (ODT == H3K_F16 ? f16_to_f32(b) : bf16_to_f32(b)));
+    }
+    bits[e] = ODT == H3K_F16 ? f32_to_f16_bits(y) : f32_to_bf16_bits(y);
+  }
+  uint16_t* const o = out + static_cast<int64_t>(m) * ldo + n0;
+  if (vec_out && n0 + 16 <= N) {
+    u32x4 w0, w1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w0[e] = bits[2 * e] | (bits[2 * e + 1] << 16);
+      w1[e] = bits[8 + 2 * e] | (bits[8 + 2 * e + 1] << 16);
+    }
+    reinterpret_cast<u32x4*>(o)[0] = w0;
+    reinterpret_cast<u32x4*>(o)[1] = w1;
+  } else {
+    for (int e = 0; e < 16 && n0 + e < N; ++e) o[e] = static_cast<uint16_t>(bits[e]);
+  }
+}
+
 template <int ODT, bool EAGER, int EPI>
 static void launch(const int8_t* a, int64_t lda, const int8_t* bp, uint32_t bp_bytes, int nbp, int m, int n, int k,
                    const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, int grid,
-                   hipStream_t st) {
+                   int tiles_dp, int P, int KP, int32_t* part, hipStream_t st) {
   const size_t es = ODT == H3K_F32 ? 4 : 2;
   const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
   hipLaunchKernelGGL((gemm_w8p_kernel<H3K_W8P_S, ODT, EAGER, EPI>), dim3(grid), dim3(256), 0, st, a, lda, bp, bp_bytes,
-                     nbp, m, n, k, xs, sch, bias, out, ldo, acc, vec_out);
+                     nbp, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, tiles_dp, P, KP, part);
+  if constexpr (ODT != H3K_F32 && (EPI == EPI_PLAIN16 || EPI == EPI_BIAS16)) {
+    const int tiles = ((m + 255) / 256) * ((n + 255) / 256);
+    if (P > 1)
+      hipLaunchKernelGGL((w8p_fixup_kernel<ODT, EAGER>), dim3((tiles - tiles_dp) * 16), dim3(256), 0, st, part, P,
+                         tiles_dp, m, n, xs, sch, bias, static_cast<uint16_t*>(out), ldo,
+                         aligned(out, 16) && ldo % 8 == 0);
+  }
 }
 
 // ------------------------------------------------------------------------------------------ packing
@@ -573,32 +696,80 @@ int cu_count();
 // Bytes of the packed grid of an [n, k] weight (n padded to a multiple of 256: a whole output tile).
 int64_t w8p_bytes(int64_t n, int64_t k) { return (n + 255) / 256 * 256 * k; }
 
-// Whether gemm_w8p_launch serves this shape: K a multiple of 64 * S with at least 2 * S steps (the per-tile step
-// phases must not overlap), M >= 4, and the same tile-count rule as the row-major persistent kernel (at least 5/8
-// of the CUs get a 256 x 256 tile, and the last round of tiles is not mostly idle).
-bool w8p_serves(int64_t m, int64_t n, int64_t k) {
+// Work split of the persistent launch, and its cost in K-steps of a 256 x 256 tile (the model below, fitted to
+// the config-3 shapes on MI355X: a K-step ~0.8 us of one round, the split tail's partial sums ~1.1 steps per MiB
+// written and read back, ~6 steps for the fix-up launch).  Whole rounds of tiles run data-parallel (one workgroup
+// per CU).  When the last round would leave CUs idle, its `rem` tiles may be cut into P pieces of KT / P K-steps
+// each (P the largest that fits rem * P <= CUs, with pieces of whole S-step groups and at least 2 S steps), and a
+// fix-up kernel adds each tile's P partial sums: taken where the model says it is faster.  P = 1: no split.
+struct W8pPlan {
+  int grid, tiles_dp, P, KP;
+  int64_t part_bytes;
+  double steps;  // modelled time in tile K-steps
+};
+static W8pPlan w8p_plan(int64_t m, int64_t n, int64_t k) {
+  constexpr int S = H3K_W8P_S;
+  const int cus = cu_count();
+  const int tiles = static_cast<int>(((m + 255) / 256) * ((n + 255) / 256));
+  const int kt = static_cast<int>(k / 64);
+  const int rounds = tiles / cus, rem = tiles - rounds * cus;
+  W8pPlan pl{tiles < cus ? tiles : cus, tiles, 1, kt, 0, static_cast<double>((rounds + (rem > 0)) * kt)};
+  if (rem == 0) return pl;
+  for (int p = cus / rem; p >= 2; --p) {
+    if (kt % p == 0 && (kt / p) % S == 0 && kt / p >= 2 * S) {
+      const int64_t part = static_cast<int64_t>(rem) * p * 256 * 256 * 4;
+      const double steps = static_cast<double>(rounds) * kt + kt / p + 1.1 * static_cast<double>(part) / (1 << 20) + 6.0;
+      if (steps < pl.steps) pl = W8pPlan{rounds > 0 ? cus : rem * p, rounds * cus, p, kt / p, part, steps};
+      break;
+    }
+  }
+  return pl;
+}
+
+// The shapes the kernel can run at all: K a multiple of 64 * S with at least 2 * S steps (the per-tile step phases
+// must not overlap), M >= 4, N a multiple of 4, the packed grid addressable by one buffer descriptor.
+static bool w8p_runs(int64_t m, int64_t n, int64_t k) {
   constexpr int S = H3K_W8P_S;
   if (k % (64 * S) || k < 2 * S * 64 || m < 4 || n < 4 || n % 4 || m > (1 << 30) || n > (1 << 30) || k > (1 << 17)) return false;
-  if (w8p_bytes(n, k) >= (int64_t(1) << 32)) return false;
+  return w8p_bytes(n, k) < (int64_t(1) << 32);
+}
+
+// Whether the W4A8 linear takes this kernel for the shape: one it runs, more than 512 rows, at least 5/8 of the CUs
+// get a 256 x 256 tile, and its modelled time (with the split tail where that pays) is no worse than the row-major
+// pipeline's on 128 x 256 tiles.
+bool w8p_serves(int64_t m, int64_t n, int64_t k) {
+  if (!w8p_runs(m, n, k)) return false;
   const int cus = cu_count();
   const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256), tiles128x256 = ((m + 127) / 128) * ((n + 255) / 256);
-  auto fill = [cus](int64_t t) { return static_cast<double>(t) / (static_cast<double>((t + cus - 1) / cus) * cus); };
-  return m > 512 && tiles256 >= cus * 5 / 8 && fill(tiles256) >= 0.83 * fill(tiles128x256);
+  if (m <= 512 || tiles256 < cus * 5 / 8) return false;
+  // against the row-major pipeline on 128 x 256 tiles: half a tile's work per tile, at ~0.72 of this kernel's rate
+  const double pipe = static_cast<double>((tiles128x256 + cus - 1) / cus) * static_cast<double>(k / 64) * 0.5 / 0.72;
+  return w8p_plan(m, n, k).steps <= pipe;
 }
 
 // Preconditions (checked by the caller): w8p_serves(m, n, k); a and w8p 16-byte aligned, lda a multiple of 16;
 // xs, s_ch and bias 16-byte aligned.
+int64_t w8p_split_bytes(int64_t m, int64_t n, int64_t k) { return w8p_plan(m, n, k).part_bytes; }
+
+// part: the split tail's partial sums (w8p_split_bytes), or nullptr for whole tiles only.  The split serves 16-bit
+// outputs without the accumulator dump.
 void gemm_w8p_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p, const float* s_ch,
                      const void* bias, int m, int n, int k, int mode, void* out, int odt, int64_t ldo, int32_t* acc_out,
-                     hipStream_t st) {
-  const int tiles = ((m + 255) / 256) * ((n + 255) / 256);
-  const int grid = tiles < cu_count() ? tiles : cu_count();
+                     int32_t* part, hipStream_t st) {
+  W8pPlan pl = w8p_plan(m, n, k);
+  if (pl.P > 1 && (!part || acc_out || odt == H3K_F32)) {
+    const int tiles = ((m + 255) / 256) * ((n + 255) / 256);
+    pl = W8pPlan{tiles < cu_count() ? tiles : cu_count(), tiles, 1, k / 64, 0, 0.0};
+  }
+  const int grid = pl.grid;
   const uint32_t bytes = static_cast<uint32_t>(w8p_bytes(n, k));
   const int nbp = static_cast<int>((n + 255) / 256 * 8);
   const bool e = mode == H3K_MODE_EAGER;
-#define H3K_L(D, P)                                                                                              \
-  (e ? w8p::launch<D, true, P>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid, st)     \
-     : w8p::launch<D, false, P>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid, st))
+#define H3K_L(D, E)                                                                                              \
+  (e ? w8p::launch<D, true, E>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid,         \
+                               pl.tiles_dp, pl.P, pl.KP, part, st)                                                \
+     : w8p::launch<D, false, E>(a, lda, w8p, bytes, nbp, m, n, k, xs, s_ch, bias, out, ldo, acc_out, grid,        \
+                                pl.tiles_dp, pl.P, pl.KP, part, st))
   // the accumulator dump has its own instantiations (a second read of every accumulator costs registers)
   if (odt == H3K_F32) {
     if (acc_out) H3K_L(H3K_F32, w8p::EPI_ACC); else H3K_L(H3K_F32, w8p::EPI_GENERAL);
@@ -653,6 +824,41 @@ extern "C" int h3k_gemm_a8w8_packed(const int8_t* a, int64_t lda, const float* x
   if (!aligned(xs, 16) || !aligned(s_ch, 16) || (bias && !aligned(bias, 16)))
     return fail(H3K_EINVAL, "xs, s_ch and bias must be 16-byte aligned");
   gemm_w8p_launch(a, lda, xs, w8p, s_ch, bias, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), mode, out,
-                  out_dtype, ldo, acc_out, static_cast<hipStream_t>(stream));
+                  out_dtype, ldo, acc_out, nullptr, static_cast<hipStream_t>(stream));
   return check_launch("gemm_a8w8_packed");
+}
+
+extern "C" int64_t h3k_gemm_packed_split_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || !w8p_runs(m, n, k)) return 0;
+  return w8p_split_bytes(m, n, k);
+}
+
+extern "C" int h3k_gemm_a8w8_packed_ws(const int8_t* a, int64_t lda, const float* xs, const int8_t* w8p,
+                                       const float* s_ch, const void* bias, int64_t m, int64_t n, int64_t k, int mode,
+                                       void* out, int out_dtype, int64_t ldo, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+  if (m < 0 || n < 0 || k < 0) return fail(H3K_EINVAL, "bad GEMM shape");
+  if (mode != H3K_MODE_CK && mode != H3K_MODE_EAGER) return fail(H3K_EINVAL, "mode must be ck (0) or eager (1)");
+  if (out_dtype != H3K_BF16 && out_dtype != H3K_F16 && out_dtype != H3K_F32)
+    return fail(H3K_EINVAL, "out dtype code %d unsupported", out_dtype);
+  if (m == 0 || n == 0) return H3K_OK;
+  if (!w8p_runs(m, n, k))
+    return fail(H3K_EINVAL, "the packed-weight GEMM needs k a multiple of 256 (>= 512), m >= 4 and n a multiple of 4: "
+                "m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  if (lda < k || ldo < n) return fail(H3K_EINVAL, "row strides smaller than the rows");
+  if ((m - 1) * lda + k >= (int64_t(1) << 32)) return fail(H3K_EINVAL, "a spans 4 GiB or more (one buffer descriptor)");
+  if (!a || !xs || !w8p || !s_ch || !out) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(a, 16) || lda % 16 || !aligned(w8p, 16))
+    return fail(H3K_EINVAL, "int8 operands must be 16-byte aligned with 16-byte multiple row strides");
+  if (!aligned(xs, 16) || !aligned(s_ch, 16) || (bias && !aligned(bias, 16)))
+    return fail(H3K_EINVAL, "xs, s_ch and bias must be 16-byte aligned");
+  const int64_t need = w8p_split_bytes(m, n, k);
+  int32_t* part = nullptr;
+  if (need > 0 && out_dtype != H3K_F32 && static_cast<int64_t>(workspace_bytes) >= need) {  // else whole tiles only
+    if (!workspace || !aligned(workspace, 256)) return fail(H3K_EINVAL, "workspace must be 256-byte aligned");
+    part = static_cast<int32_t*>(workspace);
+  }
+  gemm_w8p_launch(a, lda, xs, w8p, s_ch, bias, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), mode, out,
+                  out_dtype, ldo, nullptr, part, static_cast<hipStream_t>(stream));
+  return check_launch("gemm_a8w8_packed_ws");
 }

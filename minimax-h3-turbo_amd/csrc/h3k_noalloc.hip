@@ -4,6 +4,9 @@
 
 #include "h3k_common.hpp"
 
+namespace h3k {
+size_t w4a8_linear_base_workspace(int64_t m, int64_t n, int64_t k);
+}
 using namespace h3k;
 
 // The scratch of h3k_w4a8_linear_noalloc: a file-scope device array, one copy per GPU the library runs on, held
@@ -38,7 +41,8 @@ extern "C" int h3k_w4a8_linear_noalloc(const void* x, int x_dtype, int64_t m, in
                                        int64_t ldq, const void* s_rel, int s_dtype, int64_t lds, const float* s_ch,
                                        const float* codebook, int64_t n, int group, int rot, const void* bias, int mode,
                                        void* out, int out_dtype, int64_t ldo, void* stream) {
-  const size_t need = h3k_w4a8_linear_workspace(m, n, k);
+  // the required part of the workspace; the packed GEMM's split tail is used when the scratch holds it as well
+  const size_t need = w4a8_linear_base_workspace(m, n, k);
   if (need > kNoAllocScratchBytes)
     return fail(H3K_ESPACE, "h3k_w4a8_linear_noalloc: m=%lld n=%lld k=%lld needs %zu bytes of scratch, the static "
                 "scratch holds %zu: split the rows or use h3k_w4a8_linear with a workspace",

@@ -45,6 +45,9 @@ SIGNATURES = {
     "h3k_decode_w4_packed": (_int, [_ptr, _i64, _ptr, _int, _i64, _ptr, _i64, _i64, _int, _ptr, _ptr]),
     "h3k_pack_w8": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr]),
     "h3k_gemm_packed_serves": (_int, [_i64, _i64, _i64]),
+    "h3k_gemm_packed_split_bytes": (_i64, [_i64, _i64, _i64]),
+    "h3k_gemm_a8w8_packed_ws": (_int, [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _int, _ptr, _int, _i64, _ptr,
+                                       _size, _ptr]),
     "h3k_gemm_a8w8_packed": (_int, [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _int, _ptr, _int, _i64, _ptr,
                                     _ptr]),
     "h3k_qk_norm_rope": (_int, [_ptr, _i64, _ptr, _i64, _i64, _int, _int, _ptr, _ptr, _ptr, _ptr, _i64, _int,
@@ -54,7 +57,7 @@ SIGNATURES = {
     "h3k_rotate_quant_heads": (_int, [_ptr, _int, _i64, _i64, _i64, _int, _i64, _int, _int, _ptr, _i64, _ptr, _ptr]),
     "h3k_rms_modulate": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr, ctypes.c_float, _ptr, _i64, _ptr]),
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _LIB: Optional[ctypes.CDLL] = None
 _LOCK = threading.Lock()

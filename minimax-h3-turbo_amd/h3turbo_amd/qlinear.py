@@ -362,10 +362,14 @@ class _HipRunner:
             return
         if (self.packed_ok and xs.data_ptr() % 16 == 0 and out.stride(0) >= self.n and m * self.k < (1 << 32)
                 and self.lib.h3k_gemm_packed_serves(m, self.n, self.k)):
-            _lib.check(self.lib.h3k_gemm_a8w8_packed(xq.data_ptr(), self.k, xs.data_ptr(), self.w8p.data_ptr(),
-                                                     self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
-                                                     _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0),
-                                                     None, _lib.stream_of(xq.device)), "h3k_gemm_a8w8_packed")
+            # the split tail's int32 partial sums, where the launch takes it (0 bytes otherwise)
+            nbytes = self.lib.h3k_gemm_packed_split_bytes(m, self.n, self.k)
+            ws = torch.empty(nbytes // 4, dtype=torch.int32, device=xq.device) if nbytes else None
+            _lib.check(self.lib.h3k_gemm_a8w8_packed_ws(xq.data_ptr(), self.k, xs.data_ptr(), self.w8p.data_ptr(),
+                                                        self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,
+                                                        _lib.MODE[self.mode], out.data_ptr(), self.ocode, out.stride(0),
+                                                        _lib.ptr(ws), nbytes, _lib.stream_of(xq.device)),
+                       "h3k_gemm_a8w8_packed_ws")
             return
         _lib.check(self.lib.h3k_gemm_a8w8(xq.data_ptr(), self.k, xs.data_ptr(), self.w8.data_ptr(), self.k,
                                           self.dw.s_ch.data_ptr(), _lib.ptr(self.bias), m, self.n, self.k,

@@ -194,3 +194,85 @@ def test_packed_entry_points_reject_what_they_do_not_serve():
     rc = lib.h3k_gemm_a8w8_packed(x.data_ptr(), 5120, x.data_ptr(), x.data_ptr(), x.data_ptr(), None, 512, 5120, 5120, 0,
                                   x.data_ptr(), _lib.BF16, 5120, None, _lib.stream_of(DEV))
     assert rc == _lib.EINVAL and b"packed" in lib.h3k_last_error()
+
+
+# Split tail: the last round's tiles cut along K, int32 partial sums added by the fix-up kernel.  Shapes where the
+# launch's cost model takes it: one round plus 64 tiles cut by M and N (P = 3), no whole round at all (P = 6), and
+# ten rounds plus 32 tiles cut by M (P = 5).
+SPLIT = [(4000, 5000, 13824), (512, 5120, 13824), (12090, 13824, 5120)]
+
+
+def run_packed_ws(xq, xs, w8p, s_ch, n, mode, odt, bias=None, ldo=None, split=True):
+    m, k = xq.shape
+    dt = {_lib.BF16: torch.bfloat16, _lib.F16: torch.float16, _lib.F32: torch.float32}[odt]
+    ldo = ldo or n
+    out_buf = torch.zeros(m, ldo, dtype=dt, device=DEV)
+    lib = _lib.load()
+    nbytes = lib.h3k_gemm_packed_split_bytes(m, n, k) if split else 0
+    ws = torch.full((max(nbytes, 4) // 4,), -7, dtype=torch.int32, device=DEV)  # stale contents: no zeroing is assumed
+    _lib.check(lib.h3k_gemm_a8w8_packed_ws(xq.data_ptr(), k, xs.data_ptr(), w8p.data_ptr(), s_ch.data_ptr(),
+                                           _lib.ptr(bias), m, n, k, _lib.MODE[mode], out_buf.data_ptr(), odt, ldo,
+                                           ws.data_ptr(), nbytes, _lib.stream_of(DEV)), "gemm packed ws")
+    return out_buf[:, :n]
+
+
+@pytest.mark.parametrize("m,n,k", SPLIT, ids=[f"m{m}_n{n}_k{k}" for m, n, k in SPLIT])
+def test_split_tail_matches_int_mm_and_whole_tiles(m, n, k):
+    print(f"split tail m={m} n={n} k={k}", flush=True)
+    lib = _lib.load()
+    assert lib.h3k_gemm_packed_split_bytes(m, n, k) > 0, "the cost model no longer splits this shape"
+    g = torch.Generator(device=DEV).manual_seed(m + n + k + 1)
+    xq = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8, device=DEV)
+    w8 = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8, device=DEV)
+    xs = torch.rand(m, 1, generator=g, device=DEV) * 0.05 + 1e-4
+    s_ch = torch.rand(n, generator=g, device=DEV) * 0.03 + 1e-4
+    w8p = pack(w8)
+    acc = torch._int_mm(xq, w8.t())
+    want = torch_epilogue(acc, xs, s_ch, "ck", torch.bfloat16)
+    got = run_packed_ws(xq, xs, w8p, s_ch, n, "ck", _lib.BF16)
+    assert torch.equal(got.contiguous().view(torch.int16), want.view(torch.int16)), "split tail, ck bf16"
+    whole = run_packed_ws(xq, xs, w8p, s_ch, n, "ck", _lib.BF16, split=False)
+    assert torch.equal(whole.contiguous().view(torch.int16), want.view(torch.int16)), "whole tiles, ck bf16"
+
+
+@pytest.mark.parametrize("mode,odt", [("eager", _lib.F16), ("ck", _lib.F16), ("eager", _lib.BF16)])
+def test_split_tail_epilogues_bias_and_strided_outputs(mode, odt):
+    m, n, k = SPLIT[0]
+    print(f"split tail epilogue mode={mode} odt={odt}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(odt * 5 + (mode == "eager"))
+    xq = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8, device=DEV)
+    w8 = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8, device=DEV)
+    xs = torch.rand(m, 1, generator=g, device=DEV) * 0.05 + 1e-4
+    s_ch = torch.rand(n, generator=g, device=DEV) * 0.03 + 1e-4
+    dt = {_lib.BF16: torch.bfloat16, _lib.F16: torch.float16}[odt]
+    bias = torch.randn(n, generator=g, device=DEV).to(dt)
+    w8p = pack(w8)
+    acc = torch._int_mm(xq, w8.t())
+    for b, ldo in ((bias, n), (None, n + 8), (bias, n + 4)):
+        got = run_packed_ws(xq, xs, w8p, s_ch, n, mode, odt, bias=b, ldo=ldo)
+        want = torch_epilogue(acc, xs, s_ch, mode, dt, b)
+        assert torch.equal(got.contiguous().view(torch.int16), want.view(torch.int16)), (b is not None, ldo)
+
+
+def test_split_tail_through_the_w4a8_linear_entry():
+    """h3k_w4a8_linear with its full workspace (split tail) against the same call with only the required part of the
+    workspace (whole tiles), on the BASELINE weight recipe: equal bit for bit."""
+    from test_gpu_qlinear import random_acts_gpu
+
+    m, n, k = 4096, 5120, 13824
+    lib = _lib.load()
+    full = lib.h3k_w4a8_linear_workspace(m, n, k)
+    split = lib.h3k_gemm_packed_split_bytes(m, n, k)
+    assert split > 0 and full == m * k + m * 4 + n * k + split
+    x = random_acts_gpu(m, k, seed=11)
+    w = random_weight_gpu(n, k, seed=12)
+    outs = []
+    for nbytes in (full, full - split):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+        _lib.check(lib.h3k_w4a8_linear(x.data_ptr(), _lib.BF16, m, k, k, w.q.data_ptr(), w.q.stride(0), w.s_rel.data_ptr(),
+                                       _lib.scale_code(w.s_rel.dtype), w.s_rel.stride(0), w.s_ch.data_ptr(),
+                                       w.codebook.data_ptr(), n, w.group_size, w.convrot, None, 0, out.data_ptr(),
+                                       _lib.BF16, n, ws.data_ptr(), nbytes, _lib.stream_of(DEV)), "w4a8 linear")
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

@@ -54,7 +54,13 @@ def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     assert lib.h3k_w4a8_linear_workspace(600, 13824, 5120) == 600 * 5120 + 2560 + 13824 * 5120
     # past the fused few-row GEMM's 32 rows no split-K accumulators are reserved: activations + scales + grid only
     assert lib.h3k_w4a8_linear_workspace(4096, 13824, 5120) == 4096 * 5120 + 4096 * 4 + 13824 * 5120
-    assert lib.h3k_w4a8_linear_workspace(4096, 5120, 13824) <= 128 << 20  # fits the no-alloc entry's scratch
+    # where the packed GEMM takes its split tail, the partial sums on top; the required part still fits the no-alloc
+    # entry's scratch
+    split = lib.h3k_gemm_packed_split_bytes(4096, 5120, 13824)
+    assert split == 64 * 3 * 256 * 256 * 4  # one round + 64 tiles, cut in 3 along K
+    base = 4096 * 13824 + 4096 * 4 + 5120 * 13824
+    assert lib.h3k_w4a8_linear_workspace(4096, 5120, 13824) == base + split and base <= 128 << 20
+    assert lib.h3k_gemm_packed_split_bytes(32768, 13824, 5120) == 0  # whole rounds only
     # the packed grid's size and the shapes its GEMM serves
     assert lib.h3k_w8_packed_bytes(33, 128) == 256 * 128 and lib.h3k_w8_packed_bytes(32, 100) == -1
     assert lib.h3k_gemm_packed_serves(32768, 13824, 5120) == 1 and lib.h3k_gemm_packed_serves(512, 13824, 5120) == 0
