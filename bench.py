@@ -437,13 +437,16 @@ def sweep_measurement(dev, steps: int):
             xs = torch.empty(m, 1, dtype=torch.float32, device=dev)
             out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
             packed = bool(lib.h3k_gemm_packed_serves(m, n, k))  # the route qlinear.linear takes
+            split = lib.h3k_gemm_packed_split_bytes(m, n, k) if packed else 0  # ... with the split tail where it pays
+            ws = torch.empty(max(split, 4) // 4, dtype=torch.int32, device=dev)
             rq = lambda: lib.h3k_rotate_quant(x.data_ptr(), _lib.BF16, m, k, k, 256, 0, xq.data_ptr(), k, xs.data_ptr(), sp)
             if packed:
                 calls = [rq,
                          lambda: lib.h3k_decode_w4_packed(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds,
                                                           dw.cb.data_ptr(), n, k, 128, w8.data_ptr(), sp),
-                         lambda: lib.h3k_gemm_a8w8_packed(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(), dw.s_ch.data_ptr(),
-                                                          None, m, n, k, 0, out.data_ptr(), _lib.BF16, n, None, sp)]
+                         lambda: lib.h3k_gemm_a8w8_packed_ws(xq.data_ptr(), k, xs.data_ptr(), w8.data_ptr(),
+                                                             dw.s_ch.data_ptr(), None, m, n, k, 0, out.data_ptr(), _lib.BF16,
+                                                             n, ws.data_ptr(), split, sp)]
             else:
                 calls = [rq,
                          lambda: lib.h3k_decode_w4(dw.q.data_ptr(), dw.ldq, dw.s.data_ptr(), dw.scode, dw.lds, dw.cb.data_ptr(),
@@ -464,7 +467,8 @@ def sweep_measurement(dev, steps: int):
             torch.cuda.synchronize()
             t = [sum(a.elapsed_time(b) for a, b in e) / len(e) for e in ev]
             ops = 2.0 * m * n * k
-            rows.append({"m": m, "k": k, "n": n, "kernel": gemm_kernel_name(m, n, k, packed, cus),
+            rows.append({"m": m, "k": k, "n": n,
+                         "kernel": gemm_kernel_name(m, n, k, packed, cus) + (" + w8p_fixup_kernel" if split else ""),
                          "rotquant_ms": round(t[0], 4), "decode_ms": round(t[1], 4),
                          "gemm_ms": round(t[2], 4), "gemm_TOPS": round(ops / (t[2] * 1e-3) / 1e12, 1),
                          "op_TOPS": round(ops / (sum(t) * 1e-3) / 1e12, 1),
@@ -515,7 +519,7 @@ def rotquant_config2(dev, steps: int = 20, rot: int = 128):
 
 def few_rows_measurement(dev, steps: int):
     """Small-M W4A8 GEMMs against HBM: the BASELINE weight shape (N=13824, K=5120) with the BASELINE recipe (group
-    128, fp16 scales) and the checkpoint format (group 16, fp8 scales), M in {16, 64, 128}.  The fused few-row GEMM
+    128, fp16 scales) and the checkpoint format (group 16, fp8 scales), M in {16, 32, 48, 64, 128}.  The fused few-row GEMM
     (h3k_gemm_w4a8: int4 decoded in registers; zero-fill, GEMM and epilogue launches when it splits K) against the
     decode + int8 GEMM pair it replaces.  HBM figure = algorithmic bytes (packed weight + scales + int8 activations
     + xs + s_ch + bf16 out) / time of the fused call: back-to-back calls between HIP events on the launch stream."""
@@ -558,7 +562,7 @@ def few_rows_measurement(dev, steps: int):
         grp = w.group_size
         sbytes = dw.s.numel() * dw.s.element_size()
         w8 = torch.empty(n, k, dtype=torch.int8, device=dev)
-        for m in (16, 64, 128):
+        for m in (16, 32, 48, 64, 128):  # the routing cut (32 rows) sits between the 32 and 48 measurements
             g = torch.Generator(device=dev).manual_seed(m)
             xq = torch.randint(-127, 128, (m, k), generator=g, device=dev, dtype=torch.int8)
             xs = torch.rand(m, 1, generator=g, device=dev) * 1e-3

@@ -166,16 +166,11 @@ void gemm_pipe_mid_launch(int cfg, const int8_t* a, int64_t lda, const float* xs
                           int64_t ldo, int32_t* acc_out, hipStream_t st);
 int cu_count();
 
-#ifndef H3K_MID_FORCE
-#define H3K_MID_FORCE -1
-#endif
-
 
 // Tile shape of the mid-size pipeline launch: the largest tile that still gives at least 9/16 of the CUs a tile.
 // Measured at M = 64-512, K = 5120 / 13824, N = 5120-15360: 120 tiles of a shape lose to 240 of the next smaller
 // one, 160 win against 320.
 static int mid_tile(int m, int n) {
-  if (H3K_MID_FORCE >= 0) return H3K_MID_FORCE;
   const int enough = cu_count() * 9 / 16;
   auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
   if (tiles(128, 256) >= enough) return H3K_MID_128x256;
@@ -183,10 +178,6 @@ static int mid_tile(int m, int n) {
   if (tiles(64, 128) >= enough) return H3K_MID_64x128;
   return H3K_MID_64x64;
 }
-
-#ifndef H3K_GEMM_PERSIST
-#define H3K_GEMM_PERSIST 1
-#endif
 
 template <int WMB, int WNB, int ODT, bool EAGER>
 static void launch_gemm(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k, const float* xs,
@@ -231,9 +222,9 @@ int gemm_a8w8_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
   const int cus = cu_count();
   const int tiles256 = ((mm + 255) / 256) * ((nn + 255) / 256), tiles128x256 = ((mm + 127) / 128) * ((nn + 255) / 256);
   auto fill = [cus](int t) { return static_cast<double>(t) / (static_cast<double>((t + cus - 1) / cus) * cus); };
-  const bool big = k % 64 == 0 && m > 512 && n >= 256 && H3K_MID_FORCE < 0 && tiles256 >= cus * 5 / 8 &&
+  const bool big = k % 64 == 0 && m > 512 && n >= 256 && tiles256 >= cus * 5 / 8 &&
                    fill(tiles256) >= 0.83 * fill(tiles128x256);
-  if (H3K_GEMM_PERSIST && big && n % 4 == 0 && k >= gemm_persist_min_k() && aligned(s_ch, 16) && aligned(xs, 16) &&
+  if (big && n % 4 == 0 && k >= gemm_persist_min_k() && aligned(s_ch, 16) && aligned(xs, 16) &&
       (bias == nullptr || aligned(bias, 16)))
     gemm_persist_launch(a, lda, xs, w8, ldw, s_ch, bias, mm, nn, kk, mode, out, out_dtype, ldo, acc_out, st);
   else if (big)

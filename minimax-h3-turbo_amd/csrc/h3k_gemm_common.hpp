@@ -39,20 +39,11 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-#ifndef H3K_PIPE_SWZ
-#define H3K_PIPE_SWZ 1
-#endif
-#ifndef H3K_PIPE_GM
-#define H3K_PIPE_GM 8
-#endif
+// Tile-rows per group of the XCD-aware tile order (4 and 16 measured no better).
+constexpr int kTileGroupRows = 8;
+
 // physical 16-byte chunk of logical chunk c in LDS row r
-__device__ __forceinline__ int swz_chunk(int r, int c) {
-#if H3K_PIPE_SWZ == 0
-  return c ^ ((r >> 1) & 3);
-#else
-  return c ^ (((r >> 1) ^ (r >> 3)) & 3);
-#endif
-}
+__device__ __forceinline__ int swz_chunk(int r, int c) { return c ^ (((r >> 1) ^ (r >> 3)) & 3); }
 __device__ __forceinline__ int swz(int r, int c) { return r * kBK + (swz_chunk(r, c) << 4); }
 
 // tile id -> (tile_m, tile_n): XCD-contiguous ranges, then groups of GM tile-rows walked column by column

@@ -69,7 +69,7 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(const int8_t* __re
 
   auto coords = [&](int it, int& m0, int& n0) {
     int tm, tn;
-    tile_coords<H3K_PIPE_GM>(static_cast<int>(blockIdx.x) + it * static_cast<int>(gridDim.x), tiles_m, tiles_n, tm, tn);
+    tile_coords<kTileGroupRows>(static_cast<int>(blockIdx.x) + it * static_cast<int>(gridDim.x), tiles_m, tiles_n, tm, tn);
     m0 = tm * BM;
     n0 = tn * BN;
   };
@@ -325,16 +325,14 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(const int8_t* __re
   }
 }
 
-#ifndef H3K_PERSIST_S
-#define H3K_PERSIST_S 4
-#endif
+constexpr int kPersistS = 4;  // ring stages (5 measured no better)
 
 template <int ODT, bool EAGER>
 static void launch(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k, const float* xs,
                    const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc, int grid, hipStream_t st) {
   const size_t es = ODT == H3K_F32 ? 4 : 2;
   const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
-  hipLaunchKernelGGL((gemm_persist_kernel<H3K_PERSIST_S, ODT, EAGER>), dim3(grid), dim3(512), 0, st, a, lda, b, ldb, m, n,
+  hipLaunchKernelGGL((gemm_persist_kernel<kPersistS, ODT, EAGER>), dim3(grid), dim3(512), 0, st, a, lda, b, ldb, m, n,
                      k, xs, sch, bias, out, ldo, acc, vec_out);
 }
 
@@ -355,7 +353,7 @@ int cu_count() {
 
 // Smallest K the persistent kernel takes: its per-tile step phases (the S-1 steps after an epilogue, the S steps
 // that issue the next tile) must not overlap.
-int gemm_persist_min_k() { return 2 * H3K_PERSIST_S * 64; }
+int gemm_persist_min_k() { return 2 * persist::kPersistS * 64; }
 
 // K % 64 == 0, K >= gemm_persist_min_k(), N % 4 == 0, N >= 256, M >= 4; operands 16-byte aligned with 16-byte
 // multiple strides, s_ch, xs and bias 16-byte aligned (checked by the caller)

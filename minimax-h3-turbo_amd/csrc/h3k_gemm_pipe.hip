@@ -53,7 +53,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
 
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_coords<H3K_PIPE_GM>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_coords<kTileGroupRows>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -221,20 +221,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
   });
 }
 
-#ifndef H3K_PIPE_CFG
-#define H3K_PIPE_CFG 0
-#endif
-
-// tile configurations: (WM, WN, WMB, WNB, S stages, U stages per barrier, workgroups per CU)
-#if H3K_PIPE_CFG == 0
-constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 4, cU = 1, cMINB = 1;  // 256 x 256, 8 waves
-#elif H3K_PIPE_CFG == 1
-constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 5, cU = 2, cMINB = 1;  // 256 x 256, 8 waves, 160 KiB
-#elif H3K_PIPE_CFG == 2
-constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 4, cU = 2, cMINB = 1;  // 256 x 256, 8 waves
-#elif H3K_PIPE_CFG == 3
-constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 5, cU = 1, cMINB = 1;  // 256 x 256, 8 waves, 160 KiB
-#endif
+// The 256 x 256 tile: (WM, WN, WMB, WNB, S stages, U stages per barrier, workgroups per CU).  5 stages and two
+// K-steps per barrier measured no better.
+constexpr int cWM = 2, cWN = 4, cWMB = 4, cWNB = 2, cS = 4, cU = 1, cMINB = 1;  // 8 waves
 
 template <int ODT, bool EAGER>
 static void launch_pipe(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
@@ -255,9 +244,8 @@ static void launch_pipe(const int8_t* a, int64_t lda, const int8_t* b, int64_t l
 }
 
 // Smaller tiles for shapes with few 256 x 256 tiles (M up to a few thousand rows): the same deep direct-to-LDS
-// pipeline, one stage per barrier.  The register-staged kernel of h3k_gemm.hip keeps a single K-step in flight
-// and is latency-bound there.
-// U K-steps per barrier where the K-step count allows it (one otherwise).
+// pipeline, U K-steps per barrier where the K-step count is a multiple of U (one otherwise).  The register-staged
+// kernel of h3k_gemm.hip keeps a single K-step in flight and is latency-bound there.
 template <int WM, int WN, int WMB, int WNB, int S, int U, int MINB, int ODT, bool EAGER>
 static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
                        const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
@@ -278,12 +266,7 @@ static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ld
 // Ring depths of the two larger mid-size tiles.  4-6 stages (128 x 256) and 3-5 (128 x 128) measured within run-to-run
 // noise of each other at M = 128-1024, K = 5120 / 13824, N = 5120-15360.  Two K-steps per barrier make the 64-row
 // tiles faster (64 x 64 +12-14 %, 64 x 128 +2-7 %) and the 128-row ones slower (-7 to -11 %).
-#ifndef H3K_MID_S_128x256
-#define H3K_MID_S_128x256 5
-#endif
-#ifndef H3K_MID_S_128x128
-#define H3K_MID_S_128x128 4
-#endif
+constexpr int kMidS128x256 = 5, kMidS128x128 = 4;
 
 
 template <int ODT, bool EAGER>
@@ -292,10 +275,10 @@ static void launch_mid_cfg(int cfg, const int8_t* a, int64_t lda, const int8_t* 
                            hipStream_t st) {
   switch (cfg) {
     case H3K_MID_128x256:  // 8 waves of 64 x 64, 5 stages of 24 KiB, one workgroup per CU
-      launch_mid<2, 4, 2, 2, H3K_MID_S_128x256, 1, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      launch_mid<2, 4, 2, 2, kMidS128x256, 1, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
     case H3K_MID_128x128:  // 4 waves of 64 x 64, 4 stages of 16 KiB, two workgroups per CU
-      launch_mid<2, 2, 2, 2, H3K_MID_S_128x128, 1, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      launch_mid<2, 2, 2, 2, kMidS128x128, 1, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
       break;
     case H3K_MID_64x128:  // 4 waves of 32 x 64, 5 stages of 12 KiB, two workgroups per CU, 2 K-steps per barrier
       launch_mid<2, 2, 1, 2, 5, 2, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);

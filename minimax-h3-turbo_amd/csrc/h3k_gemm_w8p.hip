@@ -75,9 +75,7 @@ __device__ __forceinline__ void weight_load(v4i& dst, const u32x4& rsrc, uint32_
                    : "v"(voff), "s"(rsrc), "s"(soff), "n"(OFF));
 }
 
-#ifndef H3K_W8P_EARLY
-#define H3K_W8P_EARLY 2
-#endif
+constexpr int kEarlyMfma = 2;  // MFMAs of a half-step issued before its LDS fragment reads
 
 // Epilogue variants (a template parameter, so that no per-element branch splits the epilogue's code):
 enum { EPI_PLAIN16 = 0, EPI_BIAS16 = 1, EPI_GENERAL = 2, EPI_ACC = 3 };
@@ -139,7 +137,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
       kt = KP;
     }
     int tm, tn;
-    tile_coords<H3K_PIPE_GM>(t, tiles_m, tiles_n, tm, tn);
+    tile_coords<kTileGroupRows>(t, tiles_m, tiles_n, tm, tn);
     m0 = tm * BM;
     n0 = tn * BN;
   };
@@ -513,9 +511,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     }
     // the second half's fragment reads go out behind the first MFMAs rather than at the end of the group: their
     // latency then hides under the remaining MFMAs instead of stalling the wait before the barrier
-    __builtin_amdgcn_sched_group_barrier(0x008, H3K_W8P_EARLY, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x008, kEarlyMfma, 0);  // MFMA
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);                 // LDS reads
-    __builtin_amdgcn_sched_group_barrier(0x008, 16 - H3K_W8P_EARLY, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 16 - kEarlyMfma, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkmcnt0();
     if constexpr (wait.value == W_STEADY) {
@@ -590,9 +588,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   wait_vmcnt<0>();  // no direct-to-LDS write may land after the workgroup has ended
 }
 
-#ifndef H3K_W8P_S
-#define H3K_W8P_S 4
-#endif
+constexpr int kW8pS = 4;  // steps of the weight register ring and the activation LDS ring
 
 // Split tail: the int32 partial sums of the P pieces of each tail tile added in a fixed order (exact), then the
 // kernel's 16-bit epilogue.  One workgroup per 16 rows of a tail tile; a thread owns 16 consecutive columns of a row,
@@ -606,7 +602,7 @@ __global__ __launch_bounds__(256) void w8p_fixup_kernel(const int32_t* __restric
   const int tt = static_cast<int>(blockIdx.x) >> 4, rg = static_cast<int>(blockIdx.x) & 15;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_coords<H3K_PIPE_GM>(tiles_dp + tt, tiles_m, tiles_n, tm, tn);
+  tile_coords<kTileGroupRows>(tiles_dp + tt, tiles_m, tiles_n, tm, tn);
   const int r = rg * 16 + static_cast<int>(threadIdx.x >> 4), c = static_cast<int>(threadIdx.x & 15) * 16;
   const int m = tm * BM + r, n0 = tn * BN + c;
   if (m >= M || n0 >= N) return;
@@ -659,7 +655,7 @@ static void launch(const int8_t* a, int64_t lda, const int8_t* bp, uint32_t bp_b
                    int tiles_dp, int P, int KP, int32_t* part, hipStream_t st) {
   const size_t es = ODT == H3K_F32 ? 4 : 2;
   const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
-  hipLaunchKernelGGL((gemm_w8p_kernel<H3K_W8P_S, ODT, EAGER, EPI>), dim3(grid), dim3(256), 0, st, a, lda, bp, bp_bytes,
+  hipLaunchKernelGGL((gemm_w8p_kernel<kW8pS, ODT, EAGER, EPI>), dim3(grid), dim3(256), 0, st, a, lda, bp, bp_bytes,
                      nbp, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, tiles_dp, P, KP, part);
   if constexpr (ODT != H3K_F32 && (EPI == EPI_PLAIN16 || EPI == EPI_BIAS16)) {
     const int tiles = ((m + 255) / 256) * ((n + 255) / 256);
@@ -708,7 +704,7 @@ struct W8pPlan {
   double steps;  // modelled time in tile K-steps
 };
 static W8pPlan w8p_plan(int64_t m, int64_t n, int64_t k) {
-  constexpr int S = H3K_W8P_S;
+  constexpr int S = w8p::kW8pS;
   const int cus = cu_count();
   const int tiles = static_cast<int>(((m + 255) / 256) * ((n + 255) / 256));
   const int kt = static_cast<int>(k / 64);
@@ -729,7 +725,7 @@ static W8pPlan w8p_plan(int64_t m, int64_t n, int64_t k) {
 // The shapes the kernel can run at all: K a multiple of 64 * S with at least 2 * S steps (the per-tile step phases
 // must not overlap), M >= 4, N a multiple of 4, the packed grid addressable by one buffer descriptor.
 static bool w8p_runs(int64_t m, int64_t n, int64_t k) {
-  constexpr int S = H3K_W8P_S;
+  constexpr int S = w8p::kW8pS;
   if (k % (64 * S) || k < 2 * S * 64 || m < 4 || n < 4 || n % 4 || m > (1 << 30) || n > (1 << 30) || k > (1 << 17)) return false;
   return w8p_bytes(n, k) < (int64_t(1) << 32);
 }

@@ -426,15 +426,13 @@ static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int hshif
                      static_cast<const uint16_t*>(x), rows, k, ldx, hshift, hstride, q, ldq, xs);
 }
 
-#ifndef H3K_RQ_SPLIT_ABOVE
-#define H3K_RQ_SPLIT_ABOVE 8  // rows longer than this many passes of one wavefront are split over four
-#endif
+constexpr int kRqSplitAbove = 8;  // rows longer than this many passes of one wavefront are split over four
 
 // blocks of 256 -> (passes, wavefronts per row); passes 0 when the row is too long for the fast kernel.  Few rows
 // (under 2048) are also split, to put more wavefronts on the chip.
 static void rq_plan(int blocks, int64_t rows, int& npass, int& wpr) {
   static const int buckets[] = {1, 2, 3, 4, 5, 6, 7, 8};
-  wpr = ((blocks + 3) / 4 > H3K_RQ_SPLIT_ABOVE || (rows < 2048 && blocks > 4)) ? 4 : 1;
+  wpr = ((blocks + 3) / 4 > kRqSplitAbove || (rows < 2048 && blocks > 4)) ? 4 : 1;
   const int need = (blocks + 4 * wpr - 1) / (4 * wpr);
   npass = 0;
   for (int b : buckets)
