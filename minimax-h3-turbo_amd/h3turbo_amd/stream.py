@@ -16,9 +16,10 @@ only matters for stacks larger than free HBM.  The engine is built around three 
   fill) and `retired` (recorded on the compute stream by release(), after every kernel that reads the slot has been
   enqueued).  A fill makes the copy stream wait for `retired`; acquire() makes the compute stream wait for `landed`.
 * Only host-side work needs a thread: staging a pageable block into a page-locked buffer is a CPU memcpy, and a
-  copy from pageable memory is synchronous.  A single fill thread executes the fills the model thread queues, in
-  queue order, and completes a ticket per fill; acquire() waits on the ticket (the fill has been issued to the
-  device -- or, on the CPU path, done).
+  copy from pageable memory is synchronous.  A single fill thread executes the fills the model thread queues for
+  such sources, in queue order, and completes a ticket per fill; acquire() waits on the ticket (the fill has been
+  issued to the device -- or, on the CPU path, done).  Fills from page-locked memory (registered, pinned) are
+  issued by the model thread itself, when they are scheduled: their tickets are complete at once.
 
 Host sources per streamed block ("host kind"):
     registered  the store itself is page-locked (allocated pinned): zero-copy DMA straight from its pages
@@ -399,6 +400,18 @@ class StreamingProvider:
     def _run_fill(self, slot: _Slot, b: int, retired) -> None:
         """Executed by the fill thread: the host side of the copy, then the copy itself."""
         t0 = time.perf_counter()
+        self._copy_into(slot, b, retired)
+        with self._lock:
+            self._count_fill(time.perf_counter() - t0)
+
+    def _count_fill(self, busy: float) -> None:
+        self._counts["copies"] += 1
+        self._counts["bytes"] += self.store.block_nbytes
+        self._counts["busy_s"] += busy
+
+    def _copy_into(self, slot: _Slot, b: int, retired) -> None:
+        """The host side of block b's copy into slot (staging, when its source needs it), then the copy, ordered
+        after the slot's last reader on the device (`retired`)."""
         kind, copy = self._source[b]
         stage = None
         if kind == "staged":
@@ -425,18 +438,31 @@ class StreamingProvider:
                 self._staging_free[stage] = landed
         else:
             self._transfer(slot.buf, src, False)
-        with self._lock:
-            self._counts["copies"] += 1
-            self._counts["bytes"] += self.store.block_nbytes
-            self._counts["busy_s"] += time.perf_counter() - t0
 
     def _fill(self, slot: _Slot, b: int) -> None:
-        """Queue block b into slot (lock held).  The slot forgets its previous block at once; the fill thread
-        orders the copy after the slot's last reader on the device."""
+        """Queue block b into slot (lock held).  The slot forgets its previous block at once; its copy is ordered
+        after the slot's last reader on the device.  From page-locked memory the copy is only enqueued on the copy
+        stream, with no host work, so this thread issues it at once: handed to the fill thread it waited until that
+        thread was scheduled behind the caller's Python work, and acquire() then found the copy of a prefetched
+        block not yet issued.  Sources that need host work (staging, pageable) go to the fill thread."""
         if slot.block is not None and self._holder.get(slot.block) is slot:
             del self._holder[slot.block]
         slot.block, slot.used = b, False
         self._holder[b] = slot
+        if self._gpu and self._source[b][0] in ("registered", "pinned"):
+            ticket = _Ticket()
+            t0 = time.perf_counter()
+            try:
+                self._copy_into(slot, b, slot.retired)
+            except BaseException as e:  # surfaces in this acquire() and every later one, as a fill-thread error does
+                if self._error is None:
+                    self._error = e
+                ticket.finish(e)
+            else:
+                self._count_fill(time.perf_counter() - t0)
+                ticket.finish()
+            slot.ticket = ticket
+            return
         slot.ticket = self._engine.submit(lambda s=slot, blk=b, ev=slot.retired: self._run_fill(s, blk, ev))
 
     def _window(self) -> List[int]:
