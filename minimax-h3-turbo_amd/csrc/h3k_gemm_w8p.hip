@@ -115,7 +115,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
   constexpr int BES = ODT == H3K_F32 ? 4 : 2;  // bias element bytes (the output dtype)
   constexpr int STEADY = G * (S - 2);
   static_assert(STEADY + NEPI + 1 < 64, "vmcnt allowance out of range");
-  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE + RS * SLOT * 4 + 4 * 32 * GROW * 4];
+  // staging words per wavefront: two 32-row blocks on 1 x 4 wavefronts (double-buffered 16-bit epilogue), one on 2 x 2
+  constexpr int STG_WORDS = (LAY ? 2 : 1) * 32 * GROW;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE + RS * SLOT * 4 + 4 * STG_WORDS * 4];
   float* const sscale = reinterpret_cast<float*>(smem + S * STAGE);
 
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     __asm__ volatile("" : "+v"(lane));
     const int kh = lane >> 5;
     const float* const sx = sscale + slot * SLOT;
-    float* const stg = reinterpret_cast<float*>(smem + S * STAGE + RS * SLOT * 4) + wave * (32 * GROW);
+    float* const stg = reinterpret_cast<float*>(smem + S * STAGE + RS * SLOT * 4) + wave * STG_WORDS;
     if constexpr (FAST) {
       const int c8 = wn * WCOLS + (lane % LPR) * 8;  // the lane's 8 columns, relative to the tile
       const int gcol = cn0 + c8;
@@ -295,6 +297,54 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
             bv[2 * e + 1] = ODT == H3K_F16 ? f16_to_f32(two >> 16) : bf16_to_f32(two >> 16);
           });
         }
+      }
+      if (LAY && whole) {
+        // The 32-row blocks through two staging buffers: block i + 1's accumulators go to LDS right after block i's
+        // read-back is issued, so those writes (the slower LDS direction) overlap block i's arithmetic.
+        int32_t* const sb0 = reinterpret_cast<int32_t*>(stg);
+        int32_t* const sb1 = sb0 + 32 * GROW;
+        auto stage_blk = [&](auto i, int32_t* buf) {
+          int32_t* const w = buf + (lane & 31) * GROW + kh * 4;
+          static_for<WNB>([&](auto j) {
+            static_for<4>([&](auto g) {
+              *reinterpret_cast<v4i*>(w + j * 32 + g * 8) =
+                  v4i{acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]};
+            });
+          });
+        };
+        stage_blk(std::integral_constant<int, 0>{}, sb0);
+        static_for<WMB>([&](auto i) {
+          constexpr int I = decltype(i)::value;
+          __builtin_amdgcn_sched_barrier(0);
+          wave_lds_sync();
+          const int32_t* const rp = (I % 2 ? sb1 : sb0) + (lane / LPR) * GROW + (lane % LPR) * 8;
+          const float* const xr = sx + wm * WROWS + I * 32 + lane / LPR;
+          v4i lo[NQ], hi[NQ];
+          float x[NQ];
+          static_for<NQ>([&](auto q) {
+            lo[q] = *reinterpret_cast<const v4i*>(rp + q * RPR * GROW);
+            hi[q] = *reinterpret_cast<const v4i*>(rp + q * RPR * GROW + 4);
+            x[q] = xr[q * RPR];
+          });
+          if constexpr (I + 1 < WMB) stage_blk(std::integral_constant<int, I + 1>{}, (I + 1) % 2 ? sb1 : sb0);
+          uint16_t* const obase = static_cast<uint16_t*>(out) +
+                                  static_cast<int64_t>(cm0 + wm * WROWS + I * 32 + lane / LPR) * ldo + gcol;
+          static_for<NQ>([&](auto q) {
+            const int a[8] = {lo[q][0], lo[q][1], lo[q][2], lo[q][3], hi[q][0], hi[q][1], hi[q][2], hi[q][3]};
+            float f[8];
+            static_for<8>([&](auto e) {
+              float y = scaled(a[e], x[q], sc[e]);
+              if constexpr (EPI == EPI_BIAS16)  // added after the output rounding (qlinear.py:404-405)
+                y = value_point(round16(y) + bv[e]);
+              f[e] = y;
+            });
+            const uint2 p0 = pack4({f[0], f[1], f[2], f[3]}), p1 = pack4({f[4], f[5], f[6], f[7]});
+            __builtin_nontemporal_store(u32x4{p0.x, p0.y, p1.x, p1.y},
+                                        reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(q * RPR) * ldo));
+          });
+        });
+        wave_lds_sync();  // the staging area is free before the next epilogue
+        return true;
       }
       static_for<WMB>([&](auto i) {
         __builtin_amdgcn_sched_barrier(0);
@@ -453,7 +503,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
       int lane = static_cast<int>(threadIdx.x & 63);
       __asm__ volatile("" : "+v"(lane));
       const int kh = lane >> 5;
-      int32_t* const stg = reinterpret_cast<int32_t*>(smem + S * STAGE + RS * SLOT * 4) + wave * (32 * GROW);
+      int32_t* const stg = reinterpret_cast<int32_t*>(smem + S * STAGE + RS * SLOT * 4) + wave * STG_WORDS;
       int32_t* const dst = part + static_cast<int64_t>(bid) * (BM * BN);
       static_for<WMB>([&](auto i) {
         __builtin_amdgcn_sched_barrier(0);
