@@ -42,8 +42,10 @@ __device__ __forceinline__ void lds_barrier() {
 // Tile-rows per group of the XCD-aware tile order (4 and 16 measured no better).
 constexpr int kTileGroupRows = 8;
 
-// physical 16-byte chunk of logical chunk c in LDS row r
-__device__ __forceinline__ int swz_chunk(int r, int c) { return c ^ (((r >> 1) ^ (r >> 3)) & 3); }
+// physical 16-byte chunk of logical chunk c in LDS row r (64-byte rows).  A fragment read takes one chunk of rows
+// r0 .. r0 + 31 per half-wavefront; XOR with (r >> 2) & 3 puts every phase of that ds_read_b128 on distinct banks.
+// The (r >> 1) ^ (r >> 3) form cost ~4 conflict cycles per read, about 1 % of the GEMMs' time.
+__device__ __forceinline__ int swz_chunk(int r, int c) { return c ^ ((r >> 2) & 3); }
 __device__ __forceinline__ int swz(int r, int c) { return r * kBK + (swz_chunk(r, c) << 4); }
 
 // tile id -> (tile_m, tile_n): XCD-contiguous ranges, then groups of GM tile-rows walked column by column
