@@ -75,7 +75,7 @@ __device__ __forceinline__ void weight_load(v4i& dst, const u32x4& rsrc, uint32_
                    : "v"(voff), "s"(rsrc), "s"(soff), "n"(OFF));
 }
 
-constexpr int kEarlyMfma = 2;  // MFMAs of a half-step issued before its LDS fragment reads
+constexpr int kEarlyMfma = 2;  // MFMAs of a first half-step issued before the second half's fragment reads
 
 
 // Epilogue variants (a template parameter, so that no per-element branch splits the epilogue's code):
@@ -564,11 +564,22 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     } else {
       mfma(a0, u, std::integral_constant<int, 0>{});
     }
-    // the second half's fragment reads go out behind the first MFMAs rather than at the end of the group: their
-    // latency then hides under the remaining MFMAs instead of stalling the wait before the barrier
-    __builtin_amdgcn_sched_group_barrier(0x008, kEarlyMfma, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, WMB, 0);               // LDS reads
-    __builtin_amdgcn_sched_group_barrier(0x008, WMB * WNB - kEarlyMfma, 0);
+    // The scheduling region runs from the last barrier to here: the previous step's second half (its MFMAs, with
+    // this step's first-half fragment reads one per MFMA) and this step's first half (its MFMAs, kEarlyMfma of them
+    // ahead of the second-half reads, then one read per MFMA).  Pinning the whole region keeps the second-half reads
+    // from sinking to the wait before the barrier, where the compiler's own order had put them.
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    static_for<WMB>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    });
+    __builtin_amdgcn_sched_group_barrier(0x008, WMB * WNB - 1 - WMB, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kEarlyMfma, 0);
+    static_for<WMB>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    });
+    __builtin_amdgcn_sched_group_barrier(0x008, WMB * WNB - kEarlyMfma - WMB, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkmcnt0();
     if constexpr (wait.value == W_STEADY) {
