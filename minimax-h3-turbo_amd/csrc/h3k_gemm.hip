@@ -167,14 +167,16 @@ void gemm_pipe_mid_launch(int cfg, const int8_t* a, int64_t lda, const float* xs
 int cu_count();
 
 
-// Tile shape of the mid-size pipeline launch: the largest tile that still gives at least 9/16 of the CUs a tile.
+// Tile shape of the mid-size pipeline launch: the largest tile that still gives at least 9/16 of the CUs a tile
+// (the 128 x 128 tile split over two K groups when its tiles fit in one round: +4-14 % at M = 256-512).
 // Measured at M = 64-512, K = 5120 / 13824, N = 5120-15360: 120 tiles of a shape lose to 240 of the next smaller
 // one, 160 win against 320.
 static int mid_tile(int m, int n) {
   const int enough = cu_count() * 9 / 16;
   auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
   if (tiles(128, 256) >= enough) return H3K_MID_128x256;
-  if (tiles(128, 128) >= enough) return H3K_MID_128x128;
+  // 128 x 128 tiles that all fit in one round run with two K groups: two wavefronts per SIMD instead of one
+  if (tiles(128, 128) >= enough) return tiles(128, 128) <= cu_count() ? H3K_MID_128x128_K2 : H3K_MID_128x128;
   if (tiles(64, 128) >= enough) return H3K_MID_64x128;
   return H3K_MID_64x64;
 }

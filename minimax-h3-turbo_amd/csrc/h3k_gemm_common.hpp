@@ -16,7 +16,7 @@ constexpr int kBK = 64;
 }  // namespace gemm
 
 // Tile shapes of the mid-size pipeline launch (gemm_pipe_mid_launch)
-enum { H3K_MID_64x64 = 0, H3K_MID_64x128 = 1, H3K_MID_128x128 = 2, H3K_MID_128x256 = 3 };
+enum { H3K_MID_64x64 = 0, H3K_MID_64x128 = 1, H3K_MID_128x128 = 2, H3K_MID_128x256 = 3, H3K_MID_128x128_K2 = 4 };
 
 namespace gemm {
 

@@ -15,13 +15,16 @@
 // would drain every outstanding load, prefetches included.
 //
 // LDS layout of a stage: A rows [BM][64 B] then B rows [BN][64 B].  The four 16-byte chunks of a row are
-// XOR-swizzled by (row >> 1) & 3, so the 16-byte MFMA fragment reads (32 rows x one chunk per half-wave) are
+// XOR-swizzled by (row >> 2) & 3, so the 16-byte MFMA fragment reads (32 rows x one chunk per half-wave) are
 // bank-conflict free.  A direct-to-LDS load writes 1 KiB contiguously (16 rows); the swizzle is applied on the
 // global side instead, by choosing which chunk each lane fetches.  Rows past M or N are clamped to the last
 // valid row (their products only reach output rows/columns that are never stored).
 //
-// MFMA: v_mfma_i32_32x32x32_i8.  The workgroup (WM x WN wavefronts) owns a BM x BN output tile; a wavefront
-// owns (BM / WM) x (BN / WN) as WMB x WNB blocks of 32 x 32 held in accumulation registers.  Within a K-step
+// MFMA: v_mfma_i32_32x32x32_i8.  The workgroup (KS groups of WM x WN wavefronts) owns a BM x BN output tile; a
+// wavefront owns (BM / WM) x (BN / WN) as WMB x WNB blocks of 32 x 32 held in accumulation registers.  With KS > 1
+// the groups take turns over the K-steps (group g multiplies the steps kt with kt / U = g mod KS), which puts KS
+// wavefronts on each SIMD for a tile that has a CU to itself; at the end each group adds the others' sums of the
+// 32-row blocks it stores (exact int32, through LDS) and stores those.  Within a K-step
 // the two 32-byte halves are software-pipelined: fragments of half 1 are read while half 0 multiplies, and
 // the fragments of the next K-step's half 0 while half 1 multiplies.
 #include "h3k_gemm_common.hpp"
@@ -32,8 +35,8 @@ namespace pipe {
 
 using namespace gemm;
 
-template <int WM, int WN, int WMB, int WNB, int S, int U, int MINB, int ODT, bool EAGER>
-__global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int8_t* __restrict__ A, int64_t lda,
+template <int WM, int WN, int WMB, int WNB, int S, int U, int MINB, int ODT, bool EAGER, int KS = 1>
+__global__ __launch_bounds__(KS * WM * WN * 64, MINB) void gemm_pipe_kernel(const int8_t* __restrict__ A, int64_t lda,
                                                                     const int8_t* __restrict__ B, int64_t ldb, int M,
                                                                     int N, int K, const float* __restrict__ xs,
                                                                     const float* __restrict__ sch,
@@ -41,14 +44,18 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
                                                                     void* __restrict__ out, int64_t ldo,
                                                                     int32_t* __restrict__ acc_out, bool vec_out,
                                                                     bool vec_acc) {
-  constexpr int NW = WM * WN;
+  constexpr int NT = WM * WN;  // wavefronts per K group
+  constexpr int NW = KS * NT;
+  constexpr int UP = KS * U;    // stages read between two barriers (U per group)
   constexpr int BM = 32 * WMB * WM, BN = 32 * WNB * WN;
   constexpr int STAGE = (BM + BN) * kBK;           // bytes per stage
   constexpr int D = STAGE / 1024;                  // 1 KiB direct-to-LDS loads per stage
   constexpr int DPW = D / NW;                      // ... per wavefront
   static_assert(D % NW == 0, "stage loads must split evenly over the wavefronts");
   static_assert(BM % 16 == 0 && BN % 16 == 0, "16-row load granules");
-  static_assert(U >= 1 && S >= 2 * U, "a group of U stages is read while the next U land");
+  static_assert(U >= 1 && S >= 2 * UP, "a group of UP stages is read while the next UP land");
+  static_assert(WMB % KS == 0, "each K group stores WMB / KS of the 32-row blocks");
+  static_assert(KS == 1 || NW * (WMB / KS) * WNB * 4096 <= S * STAGE, "the sums handed over fit in the ring");
   __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE];
 
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -57,7 +64,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  const int g = wave / NT, wt = wave % NT;  // K group, wavefront within the group
+  const int wm = wt / WN, wn = wt % WN;
 
   // per-lane global source of each of this wave's DPW loads (K offset added per stage)
   const int8_t* src[DPW];
@@ -103,47 +111,80 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
     });
   };
 
-  const int KT = K / kBK;
+  const int KT = K / kBK;  // a multiple of UP when KS > 1 (launcher)
   auto ring = [](int b) { return b >= S ? b - S : b; };
-  // prologue: fill the ring, wait for the first U stages
+  // prologue: fill the ring, wait for the first UP stages
   static_for<S>([&](auto s) {
     if (s < KT) issue(s, s);
   });
   int issued = KT < S ? KT : S;
-  if (KT >= S) wait_vmcnt<DPW * (S - U)>();
+  if (KT >= S) wait_vmcnt<DPW * (S - UP)>();
   else wait_vmcnt<0>();
   lds_barrier();
 
-  // Groups of U K-steps between barriers.  At the barrier closing group kt the next group's stages must have
-  // landed; stages issued after them (at most S - 2U) may still be in flight.  The U buffers just read are then
-  // refilled with the stages U groups ahead.
+  // Groups of UP K-steps between barriers, U of them per K group.  At the barrier closing group kt the next
+  // group's stages must have landed; stages issued after them (at most S - 2 UP) may still be in flight.  The UP
+  // buffers just read are then refilled with the stages UP steps ahead.
   v4i a0[WMB], b0[WNB], a1[WMB], b1[WNB];
-  read_frags(0, 0, a0, b0);
+  read_frags(g * U, 0, a0, b0);
   int buf = 0;  // ring buffer of step kt
-  for (int kt = 0; kt < KT; kt += U) {
+  for (int kt = 0; kt < KT; kt += UP) {
     static_for<U>([&](auto u) {
-      read_frags(ring(buf + u), 1, a1, b1);
+      const int sb = ring(buf + g * U + u);  // this group's stage
+      read_frags(sb, 1, a1, b1);
       mfma(a0, b0);
       if (u + 1 < U) {
-        read_frags(ring(buf + u + 1), 0, a0, b0);
+        read_frags(ring(sb + 1), 0, a0, b0);
         mfma(a1, b1);
       } else {
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkmcnt0();
-        if (issued == kt + S && kt + S <= KT) wait_vmcnt<DPW * (S - 2 * U)>();
+        if (issued == kt + S && kt + S <= KT) wait_vmcnt<DPW * (S - 2 * UP)>();
         else wait_vmcnt<0>();
         lds_barrier();
-        static_for<U>([&](auto v) {
+        static_for<UP>([&](auto v) {
           if (issued < KT) {
             issue(issued, ring(buf + v));
             ++issued;
           }
         });
-        if (kt + U < KT) read_frags(ring(buf + U), 0, a0, b0);
+        if (kt + UP < KT) read_frags(ring(buf + UP + g * U), 0, a0, b0);
         mfma(a1, b1);
       }
     });
-    buf = ring(buf + U);
+    buf = ring(buf + UP);
+  }
+  if constexpr (KS > 1) {
+    // The loop's last barrier came after every wave's last fragment read and after vmcnt(0): the ring is free.
+    // Group h hands the 32-row blocks i with i % KS != h to group i % KS, one 4 KiB slot per block, lane-major.
+    constexpr int HB = WMB / KS;  // blocks each group stores
+    int32_t* const xch = reinterpret_cast<int32_t*>(smem);
+    auto slot = [&](int h, int i, int j) { return xch + (((wt * KS + h) * HB + i / KS) * WNB + j) * 1024 + lane * 4; };
+    static_for<WMB>([&](auto i) {
+      if (i % KS != g) {
+        static_for<WNB>([&](auto j) {
+          static_for<4>([&](auto q) {
+            *reinterpret_cast<v4i*>(slot(g, i, j) + q * 256) =
+                v4i{acc[i][j][q * 4 + 0], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]};
+          });
+        });
+      }
+    });
+    wait_lgkmcnt0();
+    lds_barrier();
+    static_for<WMB>([&](auto i) {
+      if (i % KS == g) {
+        for (int h = 0; h < KS; ++h) {
+          if (h == g) continue;
+          static_for<WNB>([&](auto j) {
+            static_for<4>([&](auto q) {
+              const v4i v = *reinterpret_cast<const v4i*>(slot(h, i, j) + q * 256);
+              static_for<4>([&](auto e) { acc[i][j][q * 4 + e] += v[static_cast<int>(e)]; });
+            });
+          });
+        }
+      }
+    });
   }
 
   // ---------------------------------------------------------------- epilogue
@@ -180,14 +221,14 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void gemm_pipe_kernel(const int
     });
     static_for<WMB>([&](auto i) {
       const int m = mrow + i * 32;
-      if (m < M) {
-        static_for<4>([&](auto g) {
-          const int n = ncol + j * 32 + g * 8;
+      if (m < M && (KS == 1 || i % KS == g)) {
+        static_for<4>([&](auto q) {
+          const int n = ncol + j * 32 + q * 8;
           int a[4];
           float f[4];
           static_for<4>([&](auto e) {
-            a[e] = acc[i][j][g * 4 + e];
-            f[e] = value(a[e], xv[i], sc[g * 4 + e], bv[g * 4 + e]);
+            a[e] = acc[i][j][q * 4 + e];
+            f[e] = value(a[e], xv[i], sc[q * 4 + e], bv[q * 4 + e]);
           });
           const int64_t o = static_cast<int64_t>(m) * ldo + n;
           if (n + 3 < N && vec_out) {
@@ -246,7 +287,7 @@ static void launch_pipe(const int8_t* a, int64_t lda, const int8_t* b, int64_t l
 // Smaller tiles for shapes with few 256 x 256 tiles (M up to a few thousand rows): the same deep direct-to-LDS
 // pipeline, U K-steps per barrier where the K-step count is a multiple of U (one otherwise).  The register-staged
 // kernel of h3k_gemm.hip keeps a single K-step in flight and is latency-bound there.
-template <int WM, int WN, int WMB, int WNB, int S, int U, int MINB, int ODT, bool EAGER>
+template <int WM, int WN, int WMB, int WNB, int S, int U, int MINB, int ODT, bool EAGER, int KS = 1>
 static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb, int m, int n, int k,
                        const float* xs, const float* sch, const void* bias, void* out, int64_t ldo, int32_t* acc,
                        hipStream_t st) {
@@ -255,9 +296,10 @@ static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ld
   const size_t es = ODT == H3K_F32 ? 4 : 2;
   const bool vec_out = aligned(out, 4 * es) && ldo % 4 == 0;
   const bool vec_acc = acc == nullptr || (aligned(acc, 16) && n % 4 == 0);
-  if (U > 1 && (k / kBK) % U == 0)
-    hipLaunchKernelGGL((gemm_pipe_kernel<WM, WN, WMB, WNB, S, U, MINB, ODT, EAGER>), dim3(tiles), dim3(WM * WN * 64), 0,
-                       st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
+  if ((U > 1 || KS > 1) && (k / kBK) % (KS * U) == 0)
+    hipLaunchKernelGGL((gemm_pipe_kernel<WM, WN, WMB, WNB, S, U, MINB, ODT, EAGER, KS>), dim3(tiles),
+                       dim3(KS * WM * WN * 64), 0, st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out,
+                       vec_acc);
   else
     hipLaunchKernelGGL((gemm_pipe_kernel<WM, WN, WMB, WNB, S, 1, MINB, ODT, EAGER>), dim3(tiles), dim3(WM * WN * 64), 0,
                        st, a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, vec_out, vec_acc);
@@ -267,6 +309,10 @@ static void launch_mid(const int8_t* a, int64_t lda, const int8_t* b, int64_t ld
 // noise of each other at M = 128-1024, K = 5120 / 13824, N = 5120-15360.  Two K-steps per barrier make the 64-row
 // tiles faster (64 x 64 +12-14 %, 64 x 128 +2-7 %) and the 128-row ones slower (-7 to -11 %).
 constexpr int kMidS128x256 = 5, kMidS128x128 = 4;
+// The 128 x 128 tile with two K groups (one round of tiles, one workgroup per CU): 6 stages against 4, 7 and 8, and
+// one K-step per group between barriers against two, at M = 256-512 on the four (K, N) pairs: 4 stages lost 2-7 %
+// to the single-group tile, 6 gained 4-14 %, two K-steps per group lost 0-6 %.
+constexpr int kMidS128x128K2 = 6;
 
 
 template <int ODT, bool EAGER>
@@ -276,6 +322,10 @@ static void launch_mid_cfg(int cfg, const int8_t* a, int64_t lda, const int8_t* 
   switch (cfg) {
     case H3K_MID_128x256:  // 8 waves of 64 x 64, 5 stages of 24 KiB, one workgroup per CU
       launch_mid<2, 4, 2, 2, kMidS128x256, 1, 1, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);
+      break;
+    case H3K_MID_128x128_K2:  // 2 K groups of 4 waves of 64 x 64, 6 stages of 16 KiB, one workgroup per CU
+      launch_mid<2, 2, 2, 2, kMidS128x128K2, 1, 1, ODT, EAGER, 2>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc,
+                                                                  st);
       break;
     case H3K_MID_128x128:  // 4 waves of 64 x 64, 4 stages of 16 KiB, two workgroups per CU
       launch_mid<2, 2, 2, 2, kMidS128x128, 1, 2, ODT, EAGER>(a, lda, b, ldb, m, n, k, xs, sch, bias, out, ldo, acc, st);

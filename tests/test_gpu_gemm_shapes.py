@@ -1,5 +1,6 @@
 """The GEMM kernels (persistent and pipelined on 256 x 256 tiles where at least 160 such tiles exist on 256 CUs;
-the same pipeline on 64 x 64, 64 x 128, 128 x 128 or 128 x 256 tiles below that; the register-staged kernel for K
+the same pipeline on 64 x 64, 64 x 128, 128 x 128 (two K groups of wavefronts when the tiles fit in one round) or
+128 x 256 tiles below that; the register-staged kernel for K
 not a multiple of 64) against the CPU oracle
 on whole outputs: ragged M and N tails, K-step counts that do not divide the pipeline depth, every epilogue
 variant (ck / eager, bf16 / f16 / f32 out, bias, the int32 accumulator dump, unaligned output strides), and grids
@@ -61,11 +62,14 @@ def test_large_kernels_every_epilogue(mode, odt, with_bias):
 @pytest.mark.parametrize("m,n,k", [(200, 700, 320), (512, 5120, 576), (77, 130, 1040), (512, 8320, 256), (300, 16400, 128),
                                    (1100, 520, 640), (700, 256, 64), (513, 1028, 1344), (2304, 768, 192),
                                    (1030, 5000, 512), (600, 3000, 320), (4000, 5100, 192), (1, 300, 256), (5, 4100, 192),
-                                   (16, 2048, 1024), (256, 5120, 768)])
+                                   (16, 2048, 1024), (256, 5120, 768), (512, 5120, 1024), (520, 4100, 640),
+                                   (640, 4500, 128)])
 def test_small_m_kernel_tile_shapes(m, n, k):
     # tile shapes picked by tile count on 256 CUs: (200, 700), (1100, 520), (700, 256), (513, 1028) 64 x 64;
     # (2304, 768), (600, 3000), (256, 5120) 64 x 128 -- the last with 12 K-steps, two per barrier in steady state, so
-    # stage pairs straddle the wrap of the 5-stage ring; (512, 5120), (512, 8320) 128 x 128; (300, 16400), (1030, 5000) 128 x 256;
+    # stage pairs straddle the wrap of the 5-stage ring; (512, 5120), (512, 8320) 128 x 128 (160 tiles but 9 K-steps,
+    # and 260 tiles: one K group); (512, 5120, 1024), (520, 4100), (640, 4500) 128 x 128 with two K groups -- 16, 10
+    # and 2 K-steps, the last shorter than the 6-stage ring; (300, 16400), (1030, 5000) 128 x 256;
     # (4000, 5100): 320 tiles of 256 x 256 would leave the second round mostly idle, so 128 x 256;
     # 1, 5 and 16 rows: 64 x 64 tiles whose rows past M repeat the last row;
     # K=1040 is not a multiple of 64 (register-staged kernel)
@@ -78,6 +82,7 @@ def test_small_m_kernel_every_epilogue(mode, odt):
     run(130, 600, 448, mode, odt, True, ldo_pad=8, acc=True, seed=3)  # 64 x 64 tiles
     run(260, 4000, 256, mode, odt, True, ldo_pad=8, acc=True, seed=5)  # 64 x 128 tiles
     run(260, 4000, 768, mode, odt, True, ldo_pad=8, acc=True, seed=9)  # 64 x 128 tiles, 12 K-steps (steady pairs)
+    run(520, 4100, 384, mode, odt, True, ldo_pad=8, acc=True, seed=11)  # 128 x 128 tiles, two K groups
     run(384, 11000, 192, mode, odt, True, ldo_pad=8, acc=True, seed=4)  # 128 x 128 tiles
     run(500, 13000, 320, mode, odt, True, ldo_pad=8, acc=True, seed=6)  # 128 x 256 tiles
     run(130, 600, 464, mode, odt, True, ldo_pad=8, acc=True, seed=7)  # K % 64 != 0: register-staged kernel
