@@ -15,10 +15,12 @@
 // Why: the row-major kernels stage both operands through LDS, and at full MFMA rate their 96 KiB of fragment reads
 // plus 32 KiB of direct-to-LDS writes per K-step (256 x 256 tile) run the LDS at 60-75 % of its measured read
 // rate, a co-limiter next to the power ceiling.  Here only the activations go through LDS: a workgroup of 4
-// wavefronts (2 x 2, one per SIMD) owns a 256 x 256 tile, each wavefront 128 x 128 outputs as 4 x 4 blocks of
-// v_mfma_i32_32x32x32_i8, so per K-step the LDS sees 16 KiB of DMA writes and 32 KiB of fragment reads (48 KiB
-// instead of 128).  The weight fragments go straight from L2 into registers through buffer loads, S K-steps
-// ahead, in a register ring of S x 32 VGPRs.
+// wavefronts (one per SIMD) owns a 256 x 256 tile.  For 16-bit outputs (LAY 1) they split it 1 x 4, each wavefront
+// 256 x 64 outputs as 8 x 2 blocks of v_mfma_i32_32x32x32_i8, so no weight fragment is loaded by two wavefronts;
+// per K-step the LDS sees 16 KiB of DMA writes and 64 KiB of fragment reads.  fp32 outputs and the accumulator dump
+// (LAY 0) split it 2 x 2, 128 x 128 as 4 x 4 blocks (32 KiB of fragment reads, each weight fragment loaded twice).
+// The weight fragments go straight from L2 into registers through buffer loads, S K-steps ahead, in a register
+// ring of S x 16 VGPRs (LAY 1; S x 32 for LAY 0).
 //
 // Schedule (the persistent form of h3k_gemm_persist.hip): one workgroup per CU walks tiles t = blockIdx +
 // i * gridDim in the XCD-aware order of tile_coords; the activation DMA stream and the weight register stream both
@@ -29,10 +31,12 @@
 // full-tile epilogue, its NEPI stores.  Each tile's K loop is peeled into its first S steps, the steady steps and
 // its last S steps, so that the steady steps carry no branch at all (a taken branch stalls the wave's MFMA
 // stream while the instruction buffer refills); the first step's first MFMAs start from a zero accumulator, so
-// nothing clears the 256 accumulator registers between tiles.  The 16-bit epilogue stages each 32-row block of a
-// wavefront's raw accumulators through a private LDS area, reads 8 consecutive columns of a row per lane (their
-// scales and bias are fixed per lane for the whole tile) and stores whole 128-byte lines, non-temporally, with the
-// next tile's loads still in flight.
+// nothing clears the 256 accumulator registers between tiles.  The instruction order of the whole region between
+// two barriers is pinned (sched_group_barrier): each half-step's MFMAs with the other half's fragment reads going
+// out one per MFMA.  The 16-bit epilogue stages each 32-row block of a wavefront's raw accumulators through a
+// private LDS area (two buffers on whole tiles, the next block staged while this one is read back), reads 8
+// consecutive columns of a row per lane (their scales and bias are fixed per lane for the whole tile) and stores
+// whole 128-byte lines, non-temporally, with the next tile's loads still in flight.
 #include "h3k_gemm_common.hpp"
 
 namespace h3k {
