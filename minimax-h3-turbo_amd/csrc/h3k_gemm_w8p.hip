@@ -568,16 +568,21 @@ __global__ __launch_bounds__(256, 1) void gemm_w8p_kernel(const int8_t* __restri
     } else {
       mfma(a0, u, std::integral_constant<int, 0>{});
     }
-    // The scheduling region runs from the last barrier to here: the previous step's second half (its MFMAs, with
-    // this step's first-half fragment reads one per MFMA) and this step's first half (its MFMAs, kEarlyMfma of them
-    // ahead of the second-half reads, then one read per MFMA).  Pinning the whole region keeps the second-half reads
-    // from sinking to the wait before the barrier, where the compiler's own order had put them.
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    // The scheduling region runs from the last barrier to here: the previous step's second half (its MFMAs, the
+    // first DPW of them each behind one activation DMA issue, then this step's first-half fragment reads one per
+    // MFMA) and this step's first half (its MFMAs, kEarlyMfma of them ahead of the second-half reads, then one read
+    // per MFMA).  Pinning the whole region keeps the second-half reads from sinking to the wait before the barrier,
+    // where the compiler's own order had put them, and the DMA issues (each behind an M0 write) from holding back
+    // the first MFMAs after the barrier.
+    static_for<DPW>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read: one activation DMA issue per MFMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    });
     static_for<WMB>([&](auto) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     });
-    __builtin_amdgcn_sched_group_barrier(0x008, WMB * WNB - 1 - WMB, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, WMB * WNB - DPW - WMB, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, kEarlyMfma, 0);
     static_for<WMB>([&](auto) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
