@@ -5,50 +5,67 @@
 //   r    = 1 / sqrt(sum_e fp32(x[e])^2 / k + eps)                   fp32; the sum's order is this kernel's own
 //   n[e] = bf16(fp32(x[e]) * r * w[e])                              F.rms_norm on bf16: fp32 math, one rounding
 //   h[e] = bf16(bf16(n[e] * bf16(1 + scale[m][e])) + shift[m][e])   m = the token's modulation row
-// One wavefront per row, the row held in registers (NV 16-byte chunks per lane), so x is read once and h written
-// once; w, shift and scale are the same for every row and come from L2.
+// One workgroup per R rows (R = 4 for many rows, else 1), k / 8 threads of 8 elements: each thread issues its
+// loads of the R rows' values and of the weight words at once, and reuses the weight, shift and scale words (L2)
+// for all R rows, reloading shift and scale only where the modulation row changes.  The squares are summed per
+// thread, then across each wavefront by an xor tree, then over the wavefronts in order through LDS.  x is read once
+// and h written once.  One wavefront per row (the row in registers, the weight words reloaded per row) ran at
+// 0.34-0.41 of HBM.
 #include "h3k_common.hpp"
 
 namespace h3k {
 
-template <int NV>
-__global__ __launch_bounds__(256) void rms_modulate_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
-                                                           int k, const uint16_t* __restrict__ w,
-                                                           const uint16_t* __restrict__ shift,
-                                                           const uint16_t* __restrict__ scale, int64_t ldm,
-                                                           const int32_t* __restrict__ row_of_token, float eps,
-                                                           uint16_t* __restrict__ h, int64_t ldh) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (t >= rows) return;  // whole wavefronts
-  const uint16_t* xr = x + t * ldx;
-  u32x4 v[NV];
-  float ss = 0.0f;
+template <int R>
+__global__ __launch_bounds__(1024) void rms_modulate_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                            int k, const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ shift,
+                                                            const uint16_t* __restrict__ scale, int64_t ldm,
+                                                            const int32_t* __restrict__ row_of_token, float eps,
+                                                            uint16_t* __restrict__ h, int64_t ldh) {
+  __shared__ float s_part[R][16];
+  const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int nw = static_cast<int>(blockDim.x) >> 6;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int nr = static_cast<int>(min(static_cast<int64_t>(R), rows - t0));
+  const int e0 = tid * 8;
+  const bool on = e0 < k;
+  const u32x4 zero{0, 0, 0, 0};
+  // every load of the thread goes out at once: its 8 values of each of the R rows, then the weight words
+  u32x4 v[R];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int e0 = (i * 64 + lane) * 8;
-    v[i] = e0 < k ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + e0)) : u32x4{0, 0, 0, 0};
+  for (int r = 0; r < R; ++r)
+    v[r] = on && r < nr ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (t0 + r) * ldx + e0)) : zero;
+  const u32x4 wv = on ? *reinterpret_cast<const u32x4*>(w + e0) : zero;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float a = __uint_as_float(v[i][j] << 16), b = __uint_as_float(v[i][j] & 0xFFFF0000u);
+      const float a = __uint_as_float(v[r][j] << 16), b = __uint_as_float(v[r][j] & 0xFFFF0000u);
       ss = ss + fp32_round_point(a * a);
       ss = ss + fp32_round_point(b * b);
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
+    if (lane == 0) s_part[r][wave] = ss;
   }
+  __syncthreads();
+  if (!on) return;
+  int64_t mprev = -1;
+  u32x4 shv = zero, scv = zero;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
-  const float r = 1.0f / sqrtf(fp32_round_point(fp32_round_point(ss / static_cast<float>(k)) + eps));
-  const int64_t m = row_of_token ? row_of_token[t] : 0;
-  const uint16_t* sh = shift + m * ldm;
-  const uint16_t* sc = scale + m * ldm;
-  uint16_t* hr = h + t * ldh;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int e0 = (i * 64 + lane) * 8;
-    if (e0 >= k) continue;
-    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + e0);
-    const u32x4 shv = *reinterpret_cast<const u32x4*>(sh + e0);
-    const u32x4 scv = *reinterpret_cast<const u32x4*>(sc + e0);
+  for (int r = 0; r < R; ++r) {
+    if (r >= nr) break;
+    const int64_t t = t0 + r;
+    const int64_t m = row_of_token ? row_of_token[t] : 0;
+    if (m != mprev) {  // the modulation row's words, reloaded only when it changes
+      shv = *reinterpret_cast<const u32x4*>(shift + m * ldm + e0);
+      scv = *reinterpret_cast<const u32x4*>(scale + m * ldm + e0);
+      mprev = m;
+    }
+    float tot = s_part[r][0];
+    for (int i = 1; i < nw; ++i) tot = tot + s_part[r][i];  // the same fixed order in every thread
+    const float rr = 1.0f / sqrtf(fp32_round_point(fp32_round_point(tot / static_cast<float>(k)) + eps));
     u32x4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -56,9 +73,9 @@ __global__ __launch_bounds__(256) void rms_modulate_kernel(const uint16_t* __res
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int sft = 16 * half;
-        const float xe = bf16_to_f32((v[i][j] >> sft) & 0xFFFFu);
+        const float xe = bf16_to_f32((v[r][j] >> sft) & 0xFFFFu);
         const float we = bf16_to_f32((wv[j] >> sft) & 0xFFFFu);
-        const float n = round_bf16(fp32_round_point(fp32_round_point(xe * r) * we));
+        const float n = round_bf16(fp32_round_point(fp32_round_point(xe * rr) * we));
         const float one_plus = round_bf16(bf16_to_f32((scv[j] >> sft) & 0xFFFFu) + 1.0f);
         const float h1 = round_bf16(fp32_round_point(n * one_plus));
         const float h2 = fp32_round_point(h1 + bf16_to_f32((shv[j] >> sft) & 0xFFFFu));
@@ -66,7 +83,7 @@ __global__ __launch_bounds__(256) void rms_modulate_kernel(const uint16_t* __res
       }
       o[j] = word;
     }
-    *reinterpret_cast<u32x4*>(hr + e0) = o;
+    *reinterpret_cast<u32x4*>(h + t * ldh + e0) = o;
   }
 }
 
@@ -139,22 +156,19 @@ extern "C" int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(shift, 16) || !aligned(scale, 16) || !aligned(h, 16) || ldx % 8 ||
       ldh % 8 || ldm % 8)
     return fail(H3K_EINVAL, "rows and vectors must be 16-byte aligned (strides multiples of 8 elements)");
-  const int nv = static_cast<int>((k + 511) / 512);
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const uint16_t *xp = static_cast<const uint16_t*>(x), *wp = static_cast<const uint16_t*>(w);
-  const uint16_t *shp = static_cast<const uint16_t*>(shift), *scp = static_cast<const uint16_t*>(scale);
-  uint16_t* hp = static_cast<uint16_t*>(h);
-  const int kk = static_cast<int>(k);
-  switch (nv) {
-#define H3K_RM(NV)                                                                                                \
-  case NV:                                                                                                        \
-    hipLaunchKernelGGL((rms_modulate_kernel<NV>), grid, dim3(256), 0, st, xp, ldx, rows, kk, wp, shp, scp, ldm,    \
-                       row_of_token, eps, hp, ldh);                                                               \
-    break;
-    H3K_RM(1) H3K_RM(2) H3K_RM(3) H3K_RM(4) H3K_RM(5) H3K_RM(6) H3K_RM(7) H3K_RM(8) H3K_RM(9) H3K_RM(10) H3K_RM(11)
-    H3K_RM(12) H3K_RM(13) H3K_RM(14) H3K_RM(15) H3K_RM(16)
+  if (rows > 0x7FFFFFFF) return fail(H3K_EINVAL, "too many rows for one launch");
+  const unsigned threads = static_cast<unsigned>((k / 8 + 63) / 64 * 64);  // k <= 8192: at most 1024
+  // 4 rows per workgroup share the weight words once there are rows enough to fill the CUs (12602 x 5120: 60-65 us
+  // against 75-79 us with one row, 87-90 with 8); one row per workgroup below (777 x 3072: 4.9 against 7.1 us)
+  const bool four = rows >= 2048;
+  const dim3 grid(static_cast<unsigned>(four ? (rows + 3) / 4 : rows));
+#define H3K_RM(R)                                                                                                    \
+  hipLaunchKernelGGL((rms_modulate_kernel<R>), grid, dim3(threads), 0, static_cast<hipStream_t>(stream),            \
+                     static_cast<const uint16_t*>(x), ldx, rows, static_cast<int>(k), static_cast<const uint16_t*>(w), \
+                     static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), ldm, row_of_token, eps, \
+                     static_cast<uint16_t*>(h), ldh)
+  if (four) H3K_RM(4);
+  else H3K_RM(1);
 #undef H3K_RM
-  }
   return check_launch("rms_modulate");
 }

@@ -90,7 +90,10 @@ struct VecOf<4> { typedef uint2 T; };
 template <>
 struct VecOf<8> { typedef uint4 T; };
 
-constexpr int kSplitHPB = 4;  // head rows per half-wavefront (one per head step)
+// Head rows per half-wavefront, their loads issued together: at 12602 tokens x 40 heads x 128 (rotary half 48 / 64)
+// 8 ran 168 / 157 us, 4 ran 171 / 167 us, and one head at a time (each load behind the previous head's LDS
+// round trips) 368 / 383 us.
+constexpr int kSplitHPB = 8;
 
 template <int J>
 __global__ __launch_bounds__(256) void qkv_split_norm_rope_kernel(
@@ -112,25 +115,45 @@ __global__ __launch_bounds__(256) void qkv_split_norm_rope_kernel(
   const float* cr = cosv + t * ldcs;
   const float* sr = sinv + t * ldcs;
 
+  // The head rows of this block step are loaded together, so their latencies overlap; the per-lane norm weights
+  // and rotary factors do not depend on the head and are read once.
+  const int h0 = blockIdx.y * kSplitHPB;
+  const int nh = min(kSplitHPB, heads - h0);
+  V raw[kSplitHPB];
+#pragma unroll
+  for (int i = 0; i < kSplitHPB; ++i)
+    if (i < nh) raw[i] = *reinterpret_cast<const V*>(xrow + static_cast<int64_t>(h0 + i) * D + J * l);
+  if (part == 2) {
+#pragma unroll
+    for (int i = 0; i < kSplitHPB; ++i)
+      if (i < nh) *reinterpret_cast<V*>(orow + static_cast<int64_t>(h0 + i) * head_stride + J * l) = raw[i];
+    return;
+  }
+  float we[J], wp[J], cs[J], sn[J];
+  int pe[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int e = l + 32 * j;
+    pe[j] = e < half ? e + half : (e < 2 * half ? e - half : -1);
+    we[j] = w[e];
+    wp[j] = pe[j] >= 0 ? w[pe[j]] : 0.0f;
+    const int ri = e < half ? e : pe[j];  // the rotary index of the pair (e, pe)
+    cs[j] = pe[j] >= 0 ? cr[ri] : 0.0f;
+    sn[j] = pe[j] >= 0 ? sr[ri] : 0.0f;
+  }
+
+#pragma unroll
   for (int i = 0; i < kSplitHPB; ++i) {
-    const int h = blockIdx.y * kSplitHPB + i;
-    if (h >= heads) break;
-    const V raw = *reinterpret_cast<const V*>(xrow + static_cast<int64_t>(h) * D + J * l);
-    V* dst = reinterpret_cast<V*>(orow + static_cast<int64_t>(h) * head_stride + J * l);
-    if (part == 2) {
-      *dst = raw;
-      continue;
-    }
+    if (i >= nh) break;
+    V* dst = reinterpret_cast<V*>(orow + static_cast<int64_t>(h0 + i) * head_stride + J * l);
     wave_lds_sync();  // the previous head's reads of this row are done
-    *reinterpret_cast<V*>(in + J * l) = raw;
+    *reinterpret_cast<V*>(in + J * l) = raw[i];
     wave_lds_sync();
     float v[J], pv[J];
-    int pe[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int e = l + 32 * j;
       v[j] = bf16_to_f32(in[e]);
-      pe[j] = e < half ? e + half : (e < 2 * half ? e - half : -1);
       pv[j] = pe[j] >= 0 ? bf16_to_f32(in[pe[j]]) : 0.0f;
     }
     float partial = fp32_round_point(v[0] * v[0]);
@@ -143,15 +166,14 @@ __global__ __launch_bounds__(256) void qkv_split_norm_rope_kernel(
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int e = l + 32 * j;
-      const float n = round_bf16(fp32_round_point(fp32_round_point(v[j] * r) * w[e]));
+      const float n = round_bf16(fp32_round_point(fp32_round_point(v[j] * r) * we[j]));
       float o = n;
       if (pe[j] >= 0) {
-        const int pp = pe[j];
-        const float np = round_bf16(fp32_round_point(fp32_round_point(pv[j] * r) * w[pp]));
+        const float np = round_bf16(fp32_round_point(fp32_round_point(pv[j] * r) * wp[j]));
         if (e < half) {
-          o = fp32_round_point(n * cr[e]) - fp32_round_point(np * sr[e]);
+          o = fp32_round_point(n * cs[j]) - fp32_round_point(np * sn[j]);
         } else {
-          o = fp32_round_point(np * sr[pp]) + fp32_round_point(n * cr[pp]);
+          o = fp32_round_point(np * sn[j]) + fp32_round_point(n * cs[j]);
         }
       }
       outr[e] = static_cast<uint16_t>(f32_to_bf16_bits(o));

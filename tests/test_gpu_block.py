@@ -299,7 +299,8 @@ def _config4_weights(hidden, inner, fc1_out, ffn, g) -> BlockWeights:
 def test_fused_rms_modulate_matches_the_torch_ops(s, k, int_valued):
     """h3k_rms_modulate against F.rms_norm + the in-place modulation on the CPU (h3turbo/h3/model.py:64-65,
     106-109).  With integer-valued rows the sum of squares is exact in any order and the outputs are bit-exact;
-    on Gaussian rows the kernel's own summation order may move the norm by an ulp on a few rows."""
+    on Gaussian rows the kernel's own summation order may move the norm by an ulp on a few rows: every output is
+    then the modulation of the reference norm or of one of its two bf16 neighbours, bit for bit."""
     print(f"rms_modulate s={s} k={k} int={int_valued}", flush=True)
     g = torch.Generator().manual_seed(s + k)
     if int_valued:
@@ -316,9 +317,14 @@ def test_fused_rms_modulate_matches_the_torch_ops(s, k, int_valued):
     if int_valued:
         assert torch.equal(got, want)
     else:
-        diff = (got.float() - want.float()).abs()
-        ulp = want.float().abs().clamp_min(1e-30) * 2.0 ** -7
-        assert (diff <= ulp * 1.01 + 1e-30).all(), "more than one bf16 ulp away"
+        n = bk.rms(x, w, 1e-5)
+        bits = n.view(torch.int16)
+        neighbours = []
+        for d in (-1, 1):  # the adjacent bf16 values of each nonzero norm (zero norms come from zero inputs)
+            nb = torch.where(n != 0, (bits + d).view(torch.bfloat16), n)
+            neighbours.append(bk.modulate_(nb.clone(), shift, scale, segments))
+        ok = (got == want) | (got == neighbours[0]) | (got == neighbours[1])
+        assert ok.all(), f"{int((~ok).sum())} outputs are not the modulation of the norm or of a neighbour"
         assert (got != want).float().mean().item() < 0.01
 
 
