@@ -20,6 +20,8 @@
 // time by two LDS transposes (bf16 input, then fp64 mid-values), so every butterfly is register-local.  The
 // whole row stays in registers as rounded 16-bit values until its absmax is known; x is read once and q
 // written once.
+#include <mutex>
+
 #include "h3k_common.hpp"
 
 namespace h3k {
@@ -120,6 +122,21 @@ __device__ __forceinline__ uint32_t gelu_tanh_word(uint32_t x2) {
   return r;
 }
 
+// GELU-tanh of every 16-bit input, one table per activation dtype (0 bf16, 1 f16), filled once per device by
+// gelu_lut_kernel, which runs gelu_tanh_word itself on each input: the table is that function, value for value.
+// The activation-fused quantiser then reads two table entries per word instead of evaluating tanhf twice.
+__device__ uint16_t g_gelu_lut[2][65536];
+
+template <bool F16>
+__global__ __launch_bounds__(256) void gelu_lut_kernel() {
+  const uint32_t v = blockIdx.x * 256u + threadIdx.x;  // grid 256 x 256: every 16-bit input once
+  g_gelu_lut[F16][v] = static_cast<uint16_t>(gelu_tanh_word<F16>(v) & 0xFFFFu);
+}
+
+__device__ __forceinline__ uint32_t gelu_lut_word(const uint16_t* __restrict__ lut, uint32_t x2) {
+  return static_cast<uint32_t>(lut[x2 & 0xFFFFu]) | (static_cast<uint32_t>(lut[x2 >> 16]) << 16);
+}
+
 // LDS geometry of the fast path (per wave, per 16-lane group g)
 constexpr int kInStride = 16 * 16 + 16;  // uint16 per group: 16 rows of 16 + pad (skews groups by 8 banks)
 constexpr int kMidRow = 17;              // doubles per mid-transpose row (odd: conflict-free 64-bit access)
@@ -135,7 +152,8 @@ constexpr int kMidStride = 16 * kMidRow + 4;
 template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone, int ROT = 256>
 __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __restrict__ x, int64_t rows, int k,
                                                           int64_t ldx, int hshift, int64_t hstride,
-                                                          int8_t* __restrict__ q, int64_t ldq, float* __restrict__ xs) {
+                                                          int8_t* __restrict__ q, int64_t ldq, float* __restrict__ xs,
+                                                          const uint16_t* __restrict__ lut) {
   static_assert(WPR == 1 || WPR == 4, "one row per wavefront or one row per workgroup");
   // The 16-bit input transpose and the fp64 mid transpose of a pass never overlap in time, so they share one
   // buffer: 35 KiB per workgroup instead of 44 KiB lets four workgroups (4 waves per SIMD) share a CU.
@@ -169,10 +187,18 @@ __global__ __launch_bounds__(256) void rotquant256_kernel(const uint16_t* __rest
           raw[p][1][i] = swiglu_word<F16>(raw[p][1][i], u1[i]);
         }
       } else if (ACT == kActGeluTanh) {
+        if (lut) {  // the table of gelu_tanh_word (wave-uniform choice)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          raw[p][0][i] = gelu_tanh_word<F16>(raw[p][0][i]);
-          raw[p][1][i] = gelu_tanh_word<F16>(raw[p][1][i]);
+          for (int i = 0; i < 4; ++i) {
+            raw[p][0][i] = gelu_lut_word(lut, raw[p][0][i]);
+            raw[p][1][i] = gelu_lut_word(lut, raw[p][1][i]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            raw[p][0][i] = gelu_tanh_word<F16>(raw[p][0][i]);
+            raw[p][1][i] = gelu_tanh_word<F16>(raw[p][1][i]);
+          }
         }
       }
     } else {
@@ -420,10 +446,10 @@ __global__ __launch_bounds__(256) void rot_generic_kernel(const void* __restrict
 // ------------------------------------------------------------------------------------------------ host side
 template <int NPASS, int WPR, bool F16, bool EAGER, int ACT = kActNone, int ROT = 256>
 static void launch256(const void* x, int64_t rows, int k, int64_t ldx, int hshift, int64_t hstride, int8_t* q,
-                      int64_t ldq, float* xs, hipStream_t st) {
+                      int64_t ldq, float* xs, hipStream_t st, const uint16_t* lut) {
   const dim3 grid(static_cast<unsigned>((rows + (4 / WPR) - 1) / (4 / WPR)));
   hipLaunchKernelGGL((rotquant256_kernel<NPASS, WPR, F16, EAGER, ACT, ROT>), grid, dim3(256), 0, st,
-                     static_cast<const uint16_t*>(x), rows, k, ldx, hshift, hstride, q, ldq, xs);
+                     static_cast<const uint16_t*>(x), rows, k, ldx, hshift, hstride, q, ldq, xs, lut);
 }
 
 constexpr int kRqSplitAbove = 8;  // rows longer than this many passes of one wavefront are split over four
@@ -444,11 +470,12 @@ static void rq_plan(int blocks, int64_t rows, int& npass, int& wpr) {
 
 template <bool F16, bool EAGER, int ACT = kActNone, int ROT = 256>
 static bool dispatch256(int npass, int wpr, const void* x, int64_t rows, int k, int64_t ldx, int hshift,
-                        int64_t hstride, int8_t* q, int64_t ldq, float* xs, hipStream_t st) {
+                        int64_t hstride, int8_t* q, int64_t ldq, float* xs, hipStream_t st,
+                        const uint16_t* lut = nullptr) {
   switch (npass * 8 + wpr) {
 #define H3K_CASE(P, W)      \
   case P * 8 + W:           \
-    launch256<P, W, F16, EAGER, ACT, ROT>(x, rows, k, ldx, hshift, hstride, q, ldq, xs, st); \
+    launch256<P, W, F16, EAGER, ACT, ROT>(x, rows, k, ldx, hshift, hstride, q, ldq, xs, st, lut); \
     return true;
     H3K_CASE(1, 1) H3K_CASE(2, 1) H3K_CASE(3, 1) H3K_CASE(4, 1) H3K_CASE(5, 1) H3K_CASE(6, 1) H3K_CASE(7, 1)
     H3K_CASE(8, 1) H3K_CASE(1, 4) H3K_CASE(2, 4) H3K_CASE(3, 4) H3K_CASE(4, 4) H3K_CASE(5, 4) H3K_CASE(6, 4)
@@ -567,6 +594,28 @@ extern "C" int h3k_rotate_quant_heads(const void* x, int x_dtype, int64_t rows, 
   return check_launch("rotquant256(heads)");
 }
 
+// The device's GELU table of the dtype, filled on first use: the fill kernel runs on the caller's stream, which is
+// then synchronised once, so that kernels on other streams never read a partly filled table.  A stream under graph
+// capture cannot be synchronised: until the table exists such calls evaluate tanhf in the kernel instead (the
+// same values).  nullptr means "evaluate in the kernel".
+static const uint16_t* gelu_table(bool f16, hipStream_t st) {
+  static std::mutex mu;
+  static const uint16_t* ready[64][2] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (ready[dev][f16]) return ready[dev][f16];
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  uint16_t* base = nullptr;
+  if (hipGetSymbolAddress(reinterpret_cast<void**>(&base), HIP_SYMBOL(g_gelu_lut)) != hipSuccess) return nullptr;
+  if (f16) hipLaunchKernelGGL(gelu_lut_kernel<true>, dim3(256), dim3(256), 0, st);
+  else hipLaunchKernelGGL(gelu_lut_kernel<false>, dim3(256), dim3(256), 0, st);
+  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) return nullptr;
+  ready[dev][f16] = base + (f16 ? 65536 : 0);
+  return ready[dev][f16];
+}
+
 extern "C" int h3k_rotate_quant_act(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int act,
                                     int rot, int mode, int8_t* q, int64_t ldq, float* xs, void* stream) {
   if (act != kActSwiglu && act != kActGeluTanh) return fail(H3K_EINVAL, "act must be 1 (swiglu) or 2 (gelu_tanh), got %d", act);
@@ -589,7 +638,10 @@ extern "C" int h3k_rotate_quant_act(const void* x, int x_dtype, int64_t rows, in
   const bool eager = mode == H3K_MODE_EAGER, f16 = x_dtype == H3K_F16;
   const int kk = static_cast<int>(k);
   bool ok;
-#define H3K_ACT(F, E, A) dispatch256<F, E, A>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st)
+  // bf16 only: at 12602 x 13824 the table took the kernel from 312 to 216 us; f16's finer codes spread the lookups
+  // over far more of the table, and it ran 316 against 312 us
+  const uint16_t* lut = act == kActGeluTanh && !f16 ? gelu_table(false, st) : nullptr;
+#define H3K_ACT(F, E, A) dispatch256<F, E, A>(np, wpr, x, rows, kk, ldx, 31, 0, q, ldq, xs, st, lut)
   if (act == kActSwiglu)
     ok = f16 ? (eager ? H3K_ACT(true, true, kActSwiglu) : H3K_ACT(true, false, kActSwiglu))
              : (eager ? H3K_ACT(false, true, kActSwiglu) : H3K_ACT(false, false, kActSwiglu));

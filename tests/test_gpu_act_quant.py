@@ -66,6 +66,19 @@ def test_extreme_values_and_strided_rows(act):
             assert_same(fused(x, act, mode), unfused(x.contiguous(), act, mode), f"{act} {dt} {mode}")
 
 
+def test_gelu_on_every_bf16_value():
+    """Every finite bf16 value through the bf16 GELU path (a table of the in-kernel formula, filled on the GPU on
+    first use) against the torch ops: 64 rows of 1024, each row one slice of the 65 280 finite codes (padded with
+    zeros), so every code is quantised once, and the row maxima span the whole exponent range."""
+    codes = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    finite = codes[torch.isfinite(codes.float())]
+    x = torch.zeros(64 * 1024, dtype=torch.bfloat16)
+    x[: finite.numel()] = finite
+    x = x.view(64, 1024).to(DEV)
+    for mode in ("ck", "eager"):
+        assert_same(fused(x, "gelu_tanh", mode), unfused(x, "gelu_tanh", mode), f"every bf16 value, {mode}")
+
+
 def test_swiglu_golden_vector_pins_the_chain():
     """The reference's own CPU activation for the swiglu golden case, rotated and quantised by the oracle, against
     the fused kernel on the same bf16 input."""
