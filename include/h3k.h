@@ -193,6 +193,9 @@ int h3k_w4a8_linear_noalloc(const void* x, int x_dtype, int64_t m, int64_t k, in
  *   act 2 (gelu_tanh): the quantised input is gelu(x, tanh approximation) rounded to the activation dtype (the
  *                   config-4 GELU block's fc2 input; no reference counterpart, the reference block is SwiGLU)
  * bf16/f16 x, rotation 256, k a multiple of 256 up to 32768; 16-byte aligned rows.
+ * The first bf16 gelu_tanh call on a device fills a 128 KiB table of the GELU of every bf16 value on the given
+ * stream and synchronises that stream once; a first call on a stream under graph capture evaluates the formula in
+ * the kernel instead (the same values).
  */
 int h3k_rotate_quant_act(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx, int act, int rot, int mode,
                          int8_t* q, int64_t ldq, float* xs, void* stream);
