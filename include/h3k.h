@@ -273,6 +273,18 @@ int h3k_gated_add(void* x, int64_t ldx, const void* y, int64_t ldy, const void* 
                   const int32_t* row_of_token, int64_t rows, int64_t k, void* stream);
 
 /*
+ * h3k_gated_add followed by h3k_rms_modulate of the updated rows, in one pass over x: x[t] += y[t] * gate[m], then
+ * h[t] = the RMSNorm + modulation of the new x[t] (weights w, shift[m], scale[m]), m = row_of_token[t].  Replaces
+ * the attention branch's _gate_ (h3turbo/h3/model.py:112-115) and the _rms + _scale_shift_ before fc1 (:64-65,
+ * :106-109) as _block runs them back to back (:234-242); bit-identical to the two entry points in sequence.
+ * Arguments and alignment as for those two; row_of_token must not be NULL; h must not overlap x or y.
+ */
+int h3k_gated_add_rms_modulate(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, int64_t ldg,
+                               int64_t rows, int64_t k, const void* w, const void* shift, const void* scale,
+                               int64_t ldm, const int32_t* row_of_token, float eps, void* h, int64_t ldh,
+                               void* stream);
+
+/*
  * Host -> device copy of one weight block on the streaming engine's copy stream (hipMemcpyAsync).
  * Replaces the slot copy of h3turbo/h3/stream.py:346-354 (_issue: slot.buf.copy_(src, non_blocking)).
  * src is host memory (page-locked for an asynchronous copy), dst device memory.

@@ -15,13 +15,17 @@
 
 namespace h3k {
 
-template <int R>
+// GATED: the row is first x + y * gate (the gated residual add below, same rounding), stored back into x, and that
+// row is normalised and modulated: the block's residual add followed by the next RMSNorm + modulation, x read once.
+template <int R, bool GATED>
 __global__ __launch_bounds__(1024) void rms_modulate_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
                                                             int k, const uint16_t* __restrict__ w,
                                                             const uint16_t* __restrict__ shift,
                                                             const uint16_t* __restrict__ scale, int64_t ldm,
                                                             const int32_t* __restrict__ row_of_token, float eps,
-                                                            uint16_t* __restrict__ h, int64_t ldh) {
+                                                            uint16_t* __restrict__ h, int64_t ldh,
+                                                            const uint16_t* __restrict__ y, int64_t ldy,
+                                                            const uint16_t* __restrict__ gate, int64_t ldg) {
   __shared__ float s_part[R][16];
   const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
   const int nw = static_cast<int>(blockDim.x) >> 6;
@@ -35,6 +39,35 @@ __global__ __launch_bounds__(1024) void rms_modulate_kernel(const uint16_t* __re
 #pragma unroll
   for (int r = 0; r < R; ++r)
     v[r] = on && r < nr ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (t0 + r) * ldx + e0)) : zero;
+  if constexpr (GATED) {
+    u32x4 yv[R], gv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool live = on && r < nr;
+      const int64_t mg = live && row_of_token ? row_of_token[t0 + r] : 0;
+      yv[r] = live ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(y + (t0 + r) * ldy + e0)) : zero;
+      gv[r] = live ? *reinterpret_cast<const u32x4*>(gate + mg * ldg + e0) : zero;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int sft = 16 * half;
+          const float xe = bf16_to_f32((v[r][j] >> sft) & 0xFFFFu), ye = bf16_to_f32((yv[r][j] >> sft) & 0xFFFFu);
+          const float ge = bf16_to_f32((gv[r][j] >> sft) & 0xFFFFu);
+          word |= f32_to_bf16_bits(fp32_round_point(xe + fp32_round_point(ye * ge))) << sft;
+        }
+        o[j] = word;
+      }
+      v[r] = o;
+      if (on && r < nr)
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(const_cast<uint16_t*>(x) + (t0 + r) * ldx + e0));
+    }
+  }
   const u32x4 wv = on ? *reinterpret_cast<const u32x4*>(w + e0) : zero;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -145,6 +178,26 @@ extern "C" int h3k_gated_add(void* x, int64_t ldx, const void* y, int64_t ldy, c
   return check_launch("gated_add");
 }
 
+template <bool GATED>
+static void launch_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const void* w, const void* shift,
+                                const void* scale, int64_t ldm, const int32_t* row_of_token, float eps, void* h,
+                                int64_t ldh, const void* y, int64_t ldy, const void* gate, int64_t ldg, void* stream) {
+  const unsigned threads = static_cast<unsigned>((k / 8 + 63) / 64 * 64);  // k <= 8192: at most 1024
+  // 4 rows per workgroup share the weight words once there are rows enough to fill the CUs (12602 x 5120: 60-65 us
+  // against 75-79 us with one row, 87-90 with 8); one row per workgroup below (777 x 3072: 4.9 against 7.1 us)
+  const bool four = rows >= 2048;
+  const dim3 grid(static_cast<unsigned>(four ? (rows + 3) / 4 : rows));
+#define H3K_RM(R)                                                                                                    \
+  hipLaunchKernelGGL((rms_modulate_kernel<R, GATED>), grid, dim3(threads), 0, static_cast<hipStream_t>(stream),     \
+                     static_cast<const uint16_t*>(x), ldx, rows, static_cast<int>(k), static_cast<const uint16_t*>(w), \
+                     static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), ldm, row_of_token, eps, \
+                     static_cast<uint16_t*>(h), ldh, static_cast<const uint16_t*>(y), ldy,                         \
+                     static_cast<const uint16_t*>(gate), ldg)
+  if (four) H3K_RM(4);
+  else H3K_RM(1);
+#undef H3K_RM
+}
+
 extern "C" int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const void* w, const void* shift,
                                 const void* scale, int64_t ldm, const int32_t* row_of_token, float eps, void* h,
                                 int64_t ldh, void* stream) {
@@ -157,18 +210,25 @@ extern "C" int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_
       ldh % 8 || ldm % 8)
     return fail(H3K_EINVAL, "rows and vectors must be 16-byte aligned (strides multiples of 8 elements)");
   if (rows > 0x7FFFFFFF) return fail(H3K_EINVAL, "too many rows for one launch");
-  const unsigned threads = static_cast<unsigned>((k / 8 + 63) / 64 * 64);  // k <= 8192: at most 1024
-  // 4 rows per workgroup share the weight words once there are rows enough to fill the CUs (12602 x 5120: 60-65 us
-  // against 75-79 us with one row, 87-90 with 8); one row per workgroup below (777 x 3072: 4.9 against 7.1 us)
-  const bool four = rows >= 2048;
-  const dim3 grid(static_cast<unsigned>(four ? (rows + 3) / 4 : rows));
-#define H3K_RM(R)                                                                                                    \
-  hipLaunchKernelGGL((rms_modulate_kernel<R>), grid, dim3(threads), 0, static_cast<hipStream_t>(stream),            \
-                     static_cast<const uint16_t*>(x), ldx, rows, static_cast<int>(k), static_cast<const uint16_t*>(w), \
-                     static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), ldm, row_of_token, eps, \
-                     static_cast<uint16_t*>(h), ldh)
-  if (four) H3K_RM(4);
-  else H3K_RM(1);
-#undef H3K_RM
+  launch_rms_modulate<false>(x, ldx, rows, k, w, shift, scale, ldm, row_of_token, eps, h, ldh, nullptr, 0, nullptr, 0,
+                             stream);
   return check_launch("rms_modulate");
+}
+
+extern "C" int h3k_gated_add_rms_modulate(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate,
+                                          int64_t ldg, int64_t rows, int64_t k, const void* w, const void* shift,
+                                          const void* scale, int64_t ldm, const int32_t* row_of_token, float eps,
+                                          void* h, int64_t ldh, void* stream) {
+  if (rows < 0 || k <= 0 || k % 8 || k > 16 * 512)
+    return fail(H3K_EINVAL, "k=%lld must be a positive multiple of 8 up to 8192", (long long)k);
+  if (ldx < k || ldy < k || ldg < k || ldh < k || ldm < k) return fail(H3K_EINVAL, "row strides smaller than the rows");
+  if (rows == 0) return H3K_OK;
+  if (!x || !y || !gate || !w || !shift || !scale || !h || !row_of_token) return fail(H3K_EINVAL, "NULL pointer");
+  if (!aligned(x, 16) || !aligned(y, 16) || !aligned(gate, 16) || !aligned(w, 16) || !aligned(shift, 16) ||
+      !aligned(scale, 16) || !aligned(h, 16) || ldx % 8 || ldy % 8 || ldg % 8 || ldh % 8 || ldm % 8)
+    return fail(H3K_EINVAL, "rows and vectors must be 16-byte aligned (strides multiples of 8 elements)");
+  if (rows > 0x7FFFFFFF) return fail(H3K_EINVAL, "too many rows for one launch");
+  launch_rms_modulate<true>(x, ldx, rows, k, w, shift, scale, ldm, row_of_token, eps, h, ldh, y, ldy, gate, ldg,
+                            stream);
+  return check_launch("gated_add_rms_modulate");
 }

@@ -151,6 +151,38 @@ def gated_add_(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, segments: S
     return x
 
 
+def gated_add_rms_modulate(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, weight: torch.Tensor,
+                           shift: torch.Tensor, scale: torch.Tensor, eps: float, segments: Sequence[Segment],
+                           rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gated_add_(x, gate, y) then rms_modulate(x, weight, shift, scale) (h3turbo/h3/model.py:112-115, then :64-65,
+    106-109, as _block runs them between the attention and the MLP): in one HIP pass over x
+    (h3k_gated_add_rms_modulate) where both would take their fused form, bit-identical to the two in sequence;
+    otherwise the two in sequence.  Returns h; x is updated in place."""
+    k = x.shape[-1]
+    fused = (x.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16 and x.dim() == 2 and y.dim() == 2
+             and k % 8 == 0 and k <= 8192 and gate.shape[-1] == k and shift.shape[-1] == k and scale.shape[-1] == k
+             and x.stride(-1) == 1 and y.stride(-1) == 1 and x.data_ptr() % 16 == 0 and y.data_ptr() % 16 == 0
+             and (x.shape[0] <= 1 or (x.stride(0) % 8 == 0 and y.stride(0) % 8 == 0)))
+    if fused and rows is None:
+        rows = token_rows(segments, x.shape[0], x.device)
+    if not fused or rows is None:
+        gated_add_(x, gate, y, segments, rows)
+        return rms_modulate(x, weight, shift, scale, eps, segments, rows)
+    from . import _lib
+
+    h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    g = gate.reshape(-1, k).to(torch.bfloat16).contiguous()
+    w = weight.to(x.dtype).contiguous()
+    sh = shift.reshape(-1, k).to(x.dtype).contiguous()
+    sc = scale.reshape(-1, k).to(x.dtype).contiguous()
+    lib = _lib.load()
+    _lib.check(lib.h3k_gated_add_rms_modulate(x.data_ptr(), x.stride(0) if x.shape[0] > 1 else k, y.data_ptr(),
+                                              y.stride(0) if y.shape[0] > 1 else k, g.data_ptr(), k, x.shape[0], k,
+                                              w.data_ptr(), sh.data_ptr(), sc.data_ptr(), k, rows.data_ptr(), eps,
+                                              h.data_ptr(), k, _lib.stream_of(x.device)), "h3k_gated_add_rms_modulate")
+    return h
+
+
 def rope_angles(position_ids: torch.Tensor, inv_freq: torch.Tensor, device) -> torch.Tensor:
     """[S, 3] positions x [F] inverse frequencies -> fp32 angles [S, 3F], axis-major (h3turbo/h3/layout.py:264-271)."""
     pos = position_ids.to(device=device, dtype=torch.float32)
@@ -376,8 +408,7 @@ class DiTBlock:
         eps = self.cfg.norm_eps
         rows = token_rows(segments, x.shape[0], x.device) if x.is_cuda else None
         h = rms_modulate(x, w.norm1, sh_a, sc_a, eps, segments, rows)
-        gated_add_(x, g_a, self.attention(h, w, rope), segments, rows)
-        h = rms_modulate(x, w.norm2, sh_m, sc_m, eps, segments, rows)
+        h = gated_add_rms_modulate(x, g_a, self.attention(h, w, rope), w.norm2, sh_m, sc_m, eps, segments, rows)
         return gated_add_(x, g_m, self.mlp(h, w), segments, rows)
 
     __call__ = forward

@@ -142,23 +142,28 @@ def test_config4_width_block_within_the_north_star_tolerance(act):
     w = block_weights_gpu(lin, norms)
     blk = bk.DiTBlock(cfg)
     seen = {"h": []}
-    real_sdpa, real_rms_modulate = bk._sdpa, bk.rms_modulate
+    real_sdpa, real_rms_modulate, real_gated_rms = bk._sdpa, bk.rms_modulate, bk.gated_add_rms_modulate
 
     def capture_sdpa(q, k, v):  # the attention kernel's inputs and output, as the block ran them
         o = real_sdpa(q, k, v)
         seen.update(q=q[0].cpu(), k=k[0].cpu(), v=v[0].cpu(), o=o[0].cpu())
         return o
 
-    def capture_rms_modulate(*a, **kw):  # the two RMSNorm + modulation outputs
+    def capture_rms_modulate(*a, **kw):  # the two RMSNorm + modulation outputs (the second from the fused call)
         h = real_rms_modulate(*a, **kw)
         seen["h"].append(h.cpu())
         return h
 
-    bk._sdpa, bk.rms_modulate = capture_sdpa, capture_rms_modulate
+    def capture_gated_rms(*a, **kw):
+        h = real_gated_rms(*a, **kw)
+        seen["h"].append(h.cpu())
+        return h
+
+    bk._sdpa, bk.rms_modulate, bk.gated_add_rms_modulate = capture_sdpa, capture_rms_modulate, capture_gated_rms
     try:
         out = blk(x.to(DEV), w, [m.to(DEV) for m in mods], segs_gpu(segs), (cos.to(DEV), sin.to(DEV))).cpu()
     finally:
-        bk._sdpa, bk.rms_modulate = real_sdpa, real_rms_modulate
+        bk._sdpa, bk.rms_modulate, bk.gated_add_rms_modulate = real_sdpa, real_rms_modulate, real_gated_rms
     assert len(seen["h"]) == 2
     mlp = blk.mlp(x.to(DEV), w).cpu()
     print("  GPU block done; CPU oracle running", flush=True)
@@ -326,6 +331,28 @@ def test_fused_rms_modulate_matches_the_torch_ops(s, k, int_valued):
         ok = (got == want) | (got == neighbours[0]) | (got == neighbours[1])
         assert ok.all(), f"{int((~ok).sum())} outputs are not the modulation of the norm or of a neighbour"
         assert (got != want).float().mean().item() < 0.01
+
+
+@pytest.mark.parametrize("s,k", [(37, 5120), (300, 1024), (1, 5376), (4099, 768), (2050, 5120)])
+def test_gated_add_rms_modulate_equals_the_two_passes(s, k):
+    """h3k_gated_add_rms_modulate against h3k_gated_add then h3k_rms_modulate on the same inputs, bit for bit: the
+    updated residual and the modulated rows, with scalar and per-token modulation rows, below and above the
+    2048-row switch to 4 rows per workgroup, and a row count that leaves the last workgroup partly empty."""
+    print(f"gated_add_rms_modulate s={s} k={k}", flush=True)
+    g = torch.Generator().manual_seed(3 * s + k)
+    x = (torch.randn(s, k, generator=g) * torch.exp(torch.randn(s, 1, generator=g))).to(torch.bfloat16).to(DEV)
+    y = torch.randn(s, k, generator=g).to(torch.bfloat16).to(DEV)
+    gate, shift, scale = (0.3 * torch.randn(3, k, generator=g)).to(DEV), (0.1 * torch.randn(3, k, generator=g)).to(DEV), \
+        (0.1 * torch.randn(3, k, generator=g)).to(DEV)
+    w = (1 + 0.2 * torch.randn(k, generator=g)).to(DEV)
+    a, b = s // 3, 2 * s // 3
+    segments = [(0, a, 0), (a, b, torch.randint(0, 3, (b - a,), generator=g).to(DEV)), (b, s, 2)]
+    x2 = x.clone()
+    h_fused = bk.gated_add_rms_modulate(x, gate, y, w, shift, scale, 1e-5, segments)
+    bk.gated_add_(x2, gate, y, segments)
+    h_two = bk.rms_modulate(x2, w, shift, scale, 1e-5, segments)
+    assert torch.equal(x.view(torch.int16), x2.view(torch.int16)), "residual differs"
+    assert torch.equal(h_fused.view(torch.int16), h_two.view(torch.int16)), "modulated rows differ"
 
 
 @pytest.mark.parametrize("s,k", [(37, 5120), (300, 1024), (1, 5376), (4099, 768)])
