@@ -300,10 +300,12 @@ def _config4_weights(hidden, inner, fc1_out, ffn, g) -> BlockWeights:
                         norm1=ones(hidden), norm2=ones(hidden), q_norm=ones(128), k_norm=ones(128))
 
 
-@pytest.mark.parametrize("s,k,int_valued", [(37, 5120, True), (300, 1024, True), (5, 5376, True), (129, 5120, False)])
+@pytest.mark.parametrize("s,k,int_valued", [(37, 5120, True), (300, 1024, True), (5, 5376, True), (129, 5120, False),
+                                             (2051, 1024, True), (2051, 1024, False)])
 def test_fused_rms_modulate_matches_the_torch_ops(s, k, int_valued):
     """h3k_rms_modulate against F.rms_norm + the in-place modulation on the CPU (h3turbo/h3/model.py:64-65,
-    106-109).  With integer-valued rows the sum of squares is exact in any order and the outputs are bit-exact;
+    106-109), on one row per workgroup and (from 2048 rows) four, the last workgroup partly empty.  With
+    integer-valued rows the sum of squares is exact in any order and the outputs are bit-exact;
     on Gaussian rows the kernel's own summation order may move the norm by an ulp on a few rows: every output is
     then the modulation of the reference norm or of one of its two bf16 neighbours, bit for bit."""
     print(f"rms_modulate s={s} k={k} int={int_valued}", flush=True)
