@@ -611,7 +611,8 @@ static const uint16_t* gelu_table(bool f16, hipStream_t st) {
   if (hipGetSymbolAddress(reinterpret_cast<void**>(&base), HIP_SYMBOL(g_gelu_lut)) != hipSuccess) return nullptr;
   if (f16) hipLaunchKernelGGL(gelu_lut_kernel<true>, dim3(256), dim3(256), 0, st);
   else hipLaunchKernelGGL(gelu_lut_kernel<false>, dim3(256), dim3(256), 0, st);
-  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) return nullptr;
+  // peek, not get: an error pending from earlier work stays for the entry point's own launch check to report
+  if (hipPeekAtLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) return nullptr;
   ready[dev][f16] = base + (f16 ? 65536 : 0);
   return ready[dev][f16];
 }
