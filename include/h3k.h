@@ -243,12 +243,13 @@ int h3k_rotate_quant_heads(const void* x, int x_dtype, int64_t rows, int64_t k, 
  * with m = row_of_token[t] (NULL: row 0).  Replaces h3turbo/h3/model.py:64-65 (_rms) followed by :106-109
  * (_scale_shift_), as _block applies them before the qkv and fc1 projections (:234-242).
  *   x, h       bf16 [rows, k], row strides ldx / ldh; k a multiple of 8, at most 8192
- *   w          bf16 [k] norm weight; shift, scale bf16 [R, k] modulation rows, row stride ldm
+ *   w          [k] norm weight; shift, scale [R, k] modulation rows, row stride ldm; all three of vec_dtype,
+ *              H3K_BF16, or H3K_F32 (rounded to bf16 in the kernel as .to(torch.bfloat16) would, no copy needed)
  *   all pointers 16-byte aligned, strides multiples of 8 elements
  */
 int h3k_rms_modulate(const void* x, int64_t ldx, int64_t rows, int64_t k, const void* w, const void* shift,
                      const void* scale, int64_t ldm, const int32_t* row_of_token, float eps, void* h, int64_t ldh,
-                     void* stream);
+                     int vec_dtype, void* stream);
 
 /*
  * W4A8 linear with unquantised activations ("a16"): out = round_out(fp32(y * s_ch) + bias), y = xr @ levels^T with
@@ -265,24 +266,26 @@ int h3k_gemm_a16(const void* a, int a_dtype, int64_t lda, const int8_t* w8, int6
 /*
  * The DiT block's gated residual add, in place, bf16: x[t] += y[t] * gate[row_of_token[t]] per token row t, as one
  * pass.  Replaces the per-segment x[a:b].addcmul_(y[a:b], gate[row].to(x.dtype)) of _gate_,
- * h3turbo/h3/model.py:112-115.  gate is the gate already in bf16, one row of k per modulation row (stride ldg);
+ * h3turbo/h3/model.py:112-115.  gate is bf16 or fp32 (gate_dtype H3K_BF16 | H3K_F32; fp32 is rounded to bf16 in
+ * the kernel, as .to(x.dtype)), one row of k per modulation row (stride ldg);
  * row_of_token is int32 [rows].  Each element is bf16(fp32(x + y * gate)): the bf16 product is exact in fp32, so
  * this equals torch's addcmul on bf16 tensors.  k a multiple of 8, rows and strides 16-byte aligned.
  */
 int h3k_gated_add(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, int64_t ldg,
-                  const int32_t* row_of_token, int64_t rows, int64_t k, void* stream);
+                  const int32_t* row_of_token, int64_t rows, int64_t k, int gate_dtype, void* stream);
 
 /*
  * h3k_gated_add followed by h3k_rms_modulate of the updated rows, in one pass over x: x[t] += y[t] * gate[m], then
  * h[t] = the RMSNorm + modulation of the new x[t] (weights w, shift[m], scale[m]), m = row_of_token[t].  Replaces
  * the attention branch's _gate_ (h3turbo/h3/model.py:112-115) and the _rms + _scale_shift_ before fc1 (:64-65,
  * :106-109) as _block runs them back to back (:234-242); bit-identical to the two entry points in sequence.
- * Arguments and alignment as for those two; row_of_token must not be NULL; h must not overlap x or y.
+ * Arguments and alignment as for those two (gate, w, shift and scale all of vec_dtype); row_of_token must not
+ * be NULL; h must not overlap x or y.
  */
 int h3k_gated_add_rms_modulate(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, int64_t ldg,
                                int64_t rows, int64_t k, const void* w, const void* shift, const void* scale,
                                int64_t ldm, const int32_t* row_of_token, float eps, void* h, int64_t ldh,
-                               void* stream);
+                               int vec_dtype, void* stream);
 
 /*
  * Host -> device copy of one weight block on the streaming engine's copy stream (hipMemcpyAsync).

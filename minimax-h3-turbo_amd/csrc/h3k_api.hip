@@ -48,7 +48,7 @@ void gemm_w8p_launch(const int8_t* a, int64_t lda, const float* xs, const int8_t
 
 using namespace h3k;
 
-extern "C" int h3k_version(void) { return 6; }
+extern "C" int h3k_version(void) { return 7; }
 
 extern "C" const char* h3k_last_error(void) { return g_last_error.c_str(); }
 

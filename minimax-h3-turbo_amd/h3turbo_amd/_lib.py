@@ -39,9 +39,9 @@ SIGNATURES = {
     "h3k_w4a8_linear": (_int, [_ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _int, _i64, _ptr, _ptr, _i64, _int, _int,
                                _ptr, _int, _ptr, _int, _i64, _ptr, _size, _ptr]),
     "h3k_copy_h2d_async": (_int, [_ptr, _ptr, _size, _ptr]),
-    "h3k_gated_add": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr]),
+    "h3k_gated_add": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _int, _ptr]),
     "h3k_gated_add_rms_modulate": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr,
-                                          ctypes.c_float, _ptr, _i64, _ptr]),
+                                          ctypes.c_float, _ptr, _i64, _int, _ptr]),
     "h3k_gemm_a16": (_int, [_ptr, _int, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _ptr, _int, _i64, _ptr]),
     "h3k_w8_packed_bytes": (_i64, [_i64, _i64]),
     "h3k_decode_w4_packed": (_int, [_ptr, _i64, _ptr, _int, _i64, _ptr, _i64, _i64, _int, _ptr, _ptr]),
@@ -57,9 +57,10 @@ SIGNATURES = {
     "h3k_qkv_split_norm_rope": (_int, [_ptr, _i64, _i64, _int, _int, _ptr, _ptr, _ptr, _ptr, _i64, _int, ctypes.c_float,
                                        _ptr, _ptr, _ptr, _i64, _ptr]),
     "h3k_rotate_quant_heads": (_int, [_ptr, _int, _i64, _i64, _i64, _int, _i64, _int, _int, _ptr, _i64, _ptr, _ptr]),
-    "h3k_rms_modulate": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr, ctypes.c_float, _ptr, _i64, _ptr]),
+    "h3k_rms_modulate": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr, ctypes.c_float, _ptr, _i64, _int,
+                                _ptr]),
 }
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _LIB: Optional[ctypes.CDLL] = None
 _LOCK = threading.Lock()

@@ -98,6 +98,21 @@ def token_rows(segments: Sequence[Segment], s: int, device) -> Optional[torch.Te
     return rows if pos == s else None
 
 
+def _kernel_vectors(k: int, *vecs: torch.Tensor):
+    """The weight / modulation vectors of a fused block kernel as (tensors [R, k], their row strides, dtype code):
+    fp32 vectors go to the kernel as they are when all are fp32 with unit element stride, 16-byte aligned rows and
+    row strides a multiple of 8 (the kernel rounds them to bf16 as .to(torch.bfloat16) would; strided AdaLN chunks
+    need no copy); otherwise each is rounded to a contiguous bf16 copy here."""
+    from . import _lib
+
+    rows = [v.reshape(-1, k) for v in vecs]
+    if all(r.dtype == torch.float32 and r.stride(-1) == 1 and r.data_ptr() % 16 == 0
+           and (r.shape[0] == 1 or r.stride(0) % 8 == 0) for r in rows):
+        return rows, [r.stride(0) if r.shape[0] > 1 else k for r in rows], _lib.F32
+    rows = [r.to(torch.bfloat16).contiguous() for r in rows]
+    return rows, [k] * len(rows), _lib.BF16
+
+
 def rms_modulate(x: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float,
                  segments: Sequence[Segment], rows: Optional[torch.Tensor] = None) -> torch.Tensor:
     """modulate_(rms(x, weight, eps), shift, scale, segments) (h3turbo/h3/model.py:64-65, 106-109), in one HIP pass
@@ -113,13 +128,13 @@ def rms_modulate(x: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor, sca
         return modulate_(rms(x, weight, eps), shift, scale, segments)
     from . import _lib
 
+    (w, sh, sc), (_, ldsh, ldsc), vdt = _kernel_vectors(k, weight, shift, scale)
+    if ldsh != ldsc:  # one row stride serves both modulation tensors
+        (w, sh, sc), (_, ldsh, _), vdt = _kernel_vectors(k, weight.to(torch.bfloat16), shift, scale)
     h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    w = weight.to(x.dtype).contiguous()
-    sh = shift.reshape(-1, k).to(x.dtype).contiguous()
-    sc = scale.reshape(-1, k).to(x.dtype).contiguous()
     lib = _lib.load()
     _lib.check(lib.h3k_rms_modulate(x.data_ptr(), x.stride(0) if x.shape[0] > 1 else k, x.shape[0], k, w.data_ptr(),
-                                    sh.data_ptr(), sc.data_ptr(), k, rows.data_ptr(), eps, h.data_ptr(), k,
+                                    sh.data_ptr(), sc.data_ptr(), ldsh, rows.data_ptr(), eps, h.data_ptr(), k, vdt,
                                     _lib.stream_of(x.device)), "h3k_rms_modulate")
     return h
 
@@ -143,11 +158,11 @@ def gated_add_(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, segments: S
         return x
     from . import _lib
 
-    g = gate.reshape(-1, k).to(torch.bfloat16).contiguous()
+    (g,), (ldg,), gdt = _kernel_vectors(k, gate)
     lib = _lib.load()
     _lib.check(lib.h3k_gated_add(x.data_ptr(), x.stride(0) if x.shape[0] > 1 else k, y.data_ptr(),
-                                 y.stride(0) if y.shape[0] > 1 else k, g.data_ptr(), k, rows.data_ptr(), x.shape[0],
-                                 k, _lib.stream_of(x.device)), "h3k_gated_add")
+                                 y.stride(0) if y.shape[0] > 1 else k, g.data_ptr(), ldg, rows.data_ptr(), x.shape[0],
+                                 k, gdt, _lib.stream_of(x.device)), "h3k_gated_add")
     return x
 
 
@@ -170,16 +185,16 @@ def gated_add_rms_modulate(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor,
         return rms_modulate(x, weight, shift, scale, eps, segments, rows)
     from . import _lib
 
+    (g, w, sh, sc), (ldg, _, ldsh, ldsc), vdt = _kernel_vectors(k, gate, weight, shift, scale)
+    if ldsh != ldsc:  # one row stride serves both modulation tensors
+        (g, w, sh, sc), (ldg, _, ldsh, _), vdt = _kernel_vectors(k, gate, weight.to(torch.bfloat16), shift, scale)
     h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    g = gate.reshape(-1, k).to(torch.bfloat16).contiguous()
-    w = weight.to(x.dtype).contiguous()
-    sh = shift.reshape(-1, k).to(x.dtype).contiguous()
-    sc = scale.reshape(-1, k).to(x.dtype).contiguous()
     lib = _lib.load()
     _lib.check(lib.h3k_gated_add_rms_modulate(x.data_ptr(), x.stride(0) if x.shape[0] > 1 else k, y.data_ptr(),
-                                              y.stride(0) if y.shape[0] > 1 else k, g.data_ptr(), k, x.shape[0], k,
-                                              w.data_ptr(), sh.data_ptr(), sc.data_ptr(), k, rows.data_ptr(), eps,
-                                              h.data_ptr(), k, _lib.stream_of(x.device)), "h3k_gated_add_rms_modulate")
+                                              y.stride(0) if y.shape[0] > 1 else k, g.data_ptr(), ldg, x.shape[0], k,
+                                              w.data_ptr(), sh.data_ptr(), sc.data_ptr(), ldsh, rows.data_ptr(), eps,
+                                              h.data_ptr(), k, vdt, _lib.stream_of(x.device)),
+               "h3k_gated_add_rms_modulate")
     return h
 
 

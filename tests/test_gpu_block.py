@@ -335,11 +335,14 @@ def test_fused_rms_modulate_matches_the_torch_ops(s, k, int_valued):
         assert (got != want).float().mean().item() < 0.01
 
 
+@pytest.mark.parametrize("vec_bf16", [False, True])
 @pytest.mark.parametrize("s,k", [(37, 5120), (300, 1024), (1, 5376), (4099, 768), (2050, 5120)])
-def test_gated_add_rms_modulate_equals_the_two_passes(s, k):
+def test_gated_add_rms_modulate_equals_the_two_passes(s, k, vec_bf16):
     """h3k_gated_add_rms_modulate against h3k_gated_add then h3k_rms_modulate on the same inputs, bit for bit: the
     updated residual and the modulated rows, with scalar and per-token modulation rows, below and above the
-    2048-row switch to 4 rows per workgroup, and a row count that leaves the last workgroup partly empty."""
+    2048-row switch to 4 rows per workgroup, and a row count that leaves the last workgroup partly empty.  The
+    two passes take the fp32 vectors (rounded to bf16 in the kernels); with vec_bf16 the fused call takes them
+    rounded to bf16 by torch, which must give the same bits."""
     print(f"gated_add_rms_modulate s={s} k={k}", flush=True)
     g = torch.Generator().manual_seed(3 * s + k)
     x = (torch.randn(s, k, generator=g) * torch.exp(torch.randn(s, 1, generator=g))).to(torch.bfloat16).to(DEV)
@@ -350,7 +353,8 @@ def test_gated_add_rms_modulate_equals_the_two_passes(s, k):
     a, b = s // 3, 2 * s // 3
     segments = [(0, a, 0), (a, b, torch.randint(0, 3, (b - a,), generator=g).to(DEV)), (b, s, 2)]
     x2 = x.clone()
-    h_fused = bk.gated_add_rms_modulate(x, gate, y, w, shift, scale, 1e-5, segments)
+    vecs = [t.to(torch.bfloat16) if vec_bf16 else t for t in (gate, w, shift, scale)]
+    h_fused = bk.gated_add_rms_modulate(x, vecs[0], y, vecs[1], vecs[2], vecs[3], 1e-5, segments)
     bk.gated_add_(x2, gate, y, segments)
     h_two = bk.rms_modulate(x2, w, shift, scale, 1e-5, segments)
     assert torch.equal(x.view(torch.int16), x2.view(torch.int16)), "residual differs"

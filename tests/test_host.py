@@ -81,9 +81,13 @@ def test_c_abi_rejects_bad_arguments_without_touching_a_device():
     assert lib.h3k_rotate_quant_heads(None, _lib.BF16, 4, 480, 96, 96, 384, 256, 0, None, 480, None, None) == _lib.EINVAL
     assert "power of two" in lib.h3k_last_error().decode()
     # fused RMSNorm + modulation: k a multiple of 8 up to 8192
-    assert lib.h3k_rms_modulate(None, 100, 4, 100, None, None, None, 100, None, 1e-5, None, 100, None) == _lib.EINVAL
+    assert lib.h3k_rms_modulate(None, 100, 4, 100, None, None, None, 100, None, 1e-5, None, 100, 0, None) == _lib.EINVAL
     assert "multiple of 8" in lib.h3k_last_error().decode()
-    assert lib.h3k_rms_modulate(None, 5120, 0, 5120, None, None, None, 5120, None, 1e-5, None, 5120, None) == 0
+    # the weight / shift / scale vectors: bf16 or fp32 only
+    assert lib.h3k_rms_modulate(None, 5120, 4, 5120, None, None, None, 5120, None, 1e-5, None, 5120, _lib.F16,
+                                None) == _lib.EINVAL
+    assert "bf16 or f32" in lib.h3k_last_error().decode()
+    assert lib.h3k_rms_modulate(None, 5120, 0, 5120, None, None, None, 5120, None, 1e-5, None, 5120, 0, None) == 0
     # fused few-row W4A8 GEMM: at most 128 rows, k a multiple of 64, group 16 / 32 / multiple of 64
     w4 = lambda m, k, group: lib.h3k_gemm_w4a8(None, k, None, None, k // 2, None, _lib.FP8E4M3, max(1, k // group),  # noqa: E731
                                                None, group, None, None, m, 64, k, 0, None, _lib.BF16, 64, None, None,
