@@ -288,6 +288,23 @@ def _split_norm_rope_ok(qkv: torch.Tensor, heads: int, head_dim: int, rope) -> b
             and (qkv.shape[0] <= 1 or (2 * qkv.stride(0)) % vb == 0))
 
 
+_ROPE_F32: dict = {}
+
+
+def _rope_f32(cos: torch.Tensor, sin: torch.Tensor):
+    """The rope tables widened to contiguous fp32 (exact), once per pair of tables: every block of a forward passes
+    the same two tensors.  One entry, kept with the source tensors (so their ids cannot be reused while cached) and
+    their version counters (an in-place change invalidates it)."""
+    key = (id(cos), id(sin))
+    hit = _ROPE_F32.get(key)
+    if hit is not None and hit[0] is cos and hit[1] is sin and hit[2] == (cos._version, sin._version):
+        return hit[3], hit[4]
+    c, sn = cos.float().contiguous(), sin.float().contiguous()
+    _ROPE_F32.clear()
+    _ROPE_F32[key] = (cos, sin, (cos._version, sin._version), c, sn)
+    return c, sn
+
+
 def qkv_split_norm_rope(qkv: torch.Tensor, heads: int, head_dim: int, wq: torch.Tensor, wk: torch.Tensor, eps: float,
                         cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """The qkv projection output [S, 3 * heads * head_dim] -> head-major [3, heads, S, head_dim] (q, k, v) with the
@@ -298,7 +315,7 @@ def qkv_split_norm_rope(qkv: torch.Tensor, heads: int, head_dim: int, wq: torch.
 
     s = qkv.shape[0]
     out = torch.empty(3, heads, s, head_dim, dtype=qkv.dtype, device=qkv.device)
-    c, sn = cos.float().contiguous(), sin.float().contiguous()
+    c, sn = _rope_f32(cos, sin)
     w_q, w_k = wq.float().contiguous(), wk.float().contiguous()
     lib = _lib.load()
     _lib.check(lib.h3k_qkv_split_norm_rope(qkv.data_ptr(), qkv.stride(0) if s > 1 else qkv.shape[1], s, heads, head_dim,

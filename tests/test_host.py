@@ -197,3 +197,19 @@ def test_dense_weight_path_is_plain_f_linear():
     assert torch.allclose(ql.linear(x, w, chunk_tokens=4), torch.nn.functional.linear(x, w), rtol=1e-6, atol=1e-6)
     with pytest.raises(ValueError, match="do not match"):
         ql.linear(x, w[:, :40])
+
+
+def test_rope_table_widening_is_cached_per_table_pair_and_invalidated():
+    """qkv_split_norm_rope widens the rope tables to fp32 once per pair (every block of a forward passes the same
+    two tensors); an in-place change or another pair recomputes them."""
+    from h3turbo_amd import block as bk
+
+    cos, sin = torch.randn(7, 4).bfloat16(), torch.randn(7, 4).bfloat16()
+    a = bk._rope_f32(cos, sin)
+    assert bk._rope_f32(cos, sin)[0] is a[0]
+    assert torch.equal(a[0], cos.float()) and torch.equal(a[1], sin.float())
+    cos.mul_(3)
+    b = bk._rope_f32(cos, sin)
+    assert b[0] is not a[0] and torch.equal(b[0], cos.float())
+    other = bk._rope_f32(cos.clone(), sin)
+    assert other[0] is not b[0] and torch.equal(other[0], cos.float())
