@@ -294,7 +294,10 @@ _ROPE_F32: dict = {}
 def _rope_f32(cos: torch.Tensor, sin: torch.Tensor):
     """The rope tables widened to contiguous fp32 (exact), once per pair of tables: every block of a forward passes
     the same two tensors.  One entry, kept with the source tensors (so their ids cannot be reused while cached) and
-    their version counters (an in-place change invalidates it)."""
+    their version counters (an in-place change invalidates it).  Inference-mode tensors keep no version counter,
+    so they are widened on every call."""
+    if cos.is_inference() or sin.is_inference():
+        return cos.float().contiguous(), sin.float().contiguous()
     key = (id(cos), id(sin))
     hit = _ROPE_F32.get(key)
     if hit is not None and hit[0] is cos and hit[1] is sin and hit[2] == (cos._version, sin._version):

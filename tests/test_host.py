@@ -213,3 +213,8 @@ def test_rope_table_widening_is_cached_per_table_pair_and_invalidated():
     assert b[0] is not a[0] and torch.equal(b[0], cos.float())
     other = bk._rope_f32(cos.clone(), sin)
     assert other[0] is not b[0] and torch.equal(other[0], cos.float())
+    with torch.inference_mode():  # no version counter: widened every time, never cached
+        ci, si = cos.clone(), sin.clone()
+        first = bk._rope_f32(ci, si)
+        ci.mul_(2)
+        assert torch.equal(bk._rope_f32(ci, si)[0], ci.float()) and not torch.equal(first[0], ci.float())
