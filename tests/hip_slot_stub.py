@@ -1,7 +1,7 @@
 """The reference-side binding of the HIP backend: the `_run_hip` a reference maintainer adds to
 h3turbo/h3/qlinear.py next to `_run_ck` (h3turbo/h3/qlinear.py:427-429), calling the one C entry point
-h3k_w4a8_linear through ctypes.  The text of INTEGRATION.md section 2 is this function; the GPU tests call it
-exactly as written there, with only the library path filled in.
+h3k_w4a8_linear through ctypes.  The integration notes print this function as the binding to add; the GPU tests
+call it as written, with only the library path filled in.
 
 Test infrastructure: it binds the built library directly (no h3turbo_amd import), as the reference would.
 """

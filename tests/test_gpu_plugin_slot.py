@@ -1,5 +1,5 @@
 """The C entry point that fills the reference's kitchen slot (h3turbo/h3/qlinear.py:427-429), called exactly as a
-reference maintainer would call it (tests/hip_slot_stub.py, the code of INTEGRATION.md section 2).
+reference maintainer would call it (tests/hip_slot_stub.py, the binding the integration notes print).
 
 Both of h3k_w4a8_linear's routes are covered: chunks of at most 32 rows take the fused few-row GEMM (int4 decoded
 in registers), larger ones the weight decode + int8 GEMM.  Every result is bit-exact with the reference's golden
