@@ -101,21 +101,23 @@ __global__ __launch_bounds__(256) void decode_w4_lut_kernel(const uint8_t* __res
 // The same levels written in the packed layout of the large-shape GEMM (h3k_gemm_w8p.hip): 64-byte K-steps t of
 // 32-row blocks b (N padded to a multiple of 256 rows), block (t, b) 2 KiB at (t * NBP + b) * 2048 as two 1 KiB MFMA
 // fragments in which lane l holds row 32b + (l & 31), bytes 64t + 32(l >> 5) + 16h .. + 16.  A thread owns one row's
-// 32 consecutive levels (16 packed bytes in, the two 16-byte halves out), and threads are numbered in packed order,
-// so a wavefront's two stores are each 1 KiB contiguous.  Rows past n (the padding) are written as zeros.  GK: 0 for groups that are multiples of 32
-// (one scale per thread, its 16 levels as a byte table), 1 for group 16 (two tables), 2 for groups 4 and 8 (levels
-// computed per element).
+// 32 consecutive levels (16 packed bytes in, the two 16-byte halves out).  A workgroup takes K-steps 4T .. 4T + 3 of
+// one 32-row block: eight consecutive threads own a row's 128 packed bytes there, so every load instruction reads 8
+// whole 128-byte lines and every store writes 8 runs of 128 bytes (8 rows' 16 bytes, consecutive in a fragment).
+// Workgroups of one K-step each would split each line of the weight between workgroups far apart in time, and it
+// was fetched again.  Rows past n (the padding) are written as zeros.  GK: 0 for groups that are multiples of 32 (one scale per thread, its 16 levels as a byte table), 1 for
+// group 16 (two tables), 2 for groups 4 and 8 (levels computed per element).
 template <int SD, int GK>
 __global__ __launch_bounds__(256) void decode_w4_packed_kernel(const uint8_t* __restrict__ q, int64_t ldq,
                                                                const void* __restrict__ s_rel, int64_t lds,
                                                                const float* __restrict__ cb, int n, int nbp,
-                                                               int group, int8_t* __restrict__ wp, int64_t threads) {
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (u >= threads) return;
-  const int l = static_cast<int>(u & 63);
-  const int64_t bt = u >> 6;  // t * NBP + b
-  const int b = static_cast<int>(bt % nbp);
-  const int t = static_cast<int>(bt / nbp);
+                                                               int group, int8_t* __restrict__ wp, int kt) {
+  const int b = static_cast<int>(blockIdx.x % static_cast<unsigned>(nbp));
+  const int j = static_cast<int>(threadIdx.x & 7);  // 32-level chunk of the row within the 4 K-steps
+  const int t = static_cast<int>(blockIdx.x / static_cast<unsigned>(nbp)) * 4 + (j >> 1);
+  if (t >= kt) return;  // the last K-step group of a K-step count not a multiple of 4 (no cross-lane work below)
+  const int l = (j & 1) * 32 + static_cast<int>(threadIdx.x >> 3);  // the fragment lane: row l & 31, half l >> 5
+  const int64_t bt = static_cast<int64_t>(t) * nbp + b;
   const int row = b * 32 + (l & 31);
   const int k0 = t * 64 + (l >> 5) * 32;  // first of this thread's 32 levels
   int8_t* dst = wp + bt * 2048 + l * 16;
@@ -161,16 +163,16 @@ template <int SD>
 static void launch_decode_packed(const void* q, int64_t ldq, const void* s_rel, int64_t lds, const float* cb, int64_t n,
                                  int k, int group, int8_t* wp, hipStream_t st) {
   const int nbp = static_cast<int>((n + 255) / 256 * 8);
-  const int64_t threads = static_cast<int64_t>(nbp) * 32 * (k / 32);
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  const int kt = k / 64;
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(nbp) * ((kt + 3) / 4)));  // < 2^32 (host checks)
   const uint8_t* qb = static_cast<const uint8_t*>(q);
   const int nn = static_cast<int>(n);
   if (group % 32 == 0)
-    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 0>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, threads);
+    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 0>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, kt);
   else if (group == 16)
-    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 1>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, threads);
+    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 1>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, kt);
   else
-    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 2>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, threads);
+    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 2>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, kt);
 }
 
 template <int SD>
@@ -236,7 +238,8 @@ extern "C" int h3k_decode_w4_packed(const void* q, int64_t ldq, const void* s_re
     return fail(H3K_EINVAL,
                 "K=%lld must be divisible by 64 and group_size=%d; group_size >= 4 dividing 16 or a multiple of 16",
                 (long long)k, group);
-  if (n < 0 || n > (1 << 30) || k > (1 << 30) || (n + 255) / 256 * 256 * k >= (int64_t(1) << 40))
+  // The grid has (N' * K) / 8192 workgroups of 256 threads; its work-item count must stay below 2^32.
+  if (n < 0 || n > (1 << 30) || k > (1 << 30) || (n + 255) / 256 * 256 * k >= (int64_t(1) << 37))
     return fail(H3K_EINVAL, "bad n/k");
   if (ldq < k / 2 || lds < k / group) return fail(H3K_EINVAL, "row strides smaller than the rows");
   if (n == 0) return H3K_OK;
