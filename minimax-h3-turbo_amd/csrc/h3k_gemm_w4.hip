@@ -204,11 +204,20 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(const int8_t* __restrict__
 // into the workspace, then the epilogue kernel).
 constexpr int kChunk = 4;
 
+// fp8 scales with groups of 16 or 32 take each group's level table from a table of all 256 scale bytes that the
+// workgroup builds once in LDS (entry e: the 4 words build_lut_fast gives for scale byte e), one 16-byte LDS read
+// per group in place of ~70 VALU.  The scales then travel as their raw bytes.
+template <int SD, int GK>
+constexpr bool col_scale_table() {
+  return SD == H3K_FP8E4M3 && (GK == 16 || GK == 32);
+}
+
 template <int MB, int SD, int GK>
 struct ColChunk {
   u32x4 pq[kChunk];
   u32x4 pa[kChunk][2 * MB];
   float s1[kChunk], s2[kChunk];
+  uint32_t b1[kChunk], b2[kChunk];  // raw fp8 scale bytes (col_scale_table)
 };
 
 // Loads of chunk slots past the wavefront's range read its last step (valid) and are never computed; A rows past M
@@ -230,7 +239,11 @@ __device__ __forceinline__ void col_load(ColChunk<MB, SD, GK>& c, int first, int
       for (int s = 0; s < 2; ++s)
         c.pa[j][2 * b + s] = *reinterpret_cast<const u32x4*>(arow[b] + static_cast<int64_t>(t) * kBK + s * 16);
     const int k0 = t * kBK + kh * 32;
-    if (GK == 16) {
+    if (col_scale_table<SD, GK>()) {
+      const uint8_t* sbytes = static_cast<const uint8_t*>(s_rel) + srow;
+      c.b1[j] = sbytes[k0 / GK];
+      if (GK == 16) c.b2[j] = sbytes[k0 / 16 + 1];
+    } else if (GK == 16) {
       c.s1[j] = load_scale<SD>(s_rel, srow + k0 / 16);
       c.s2[j] = load_scale<SD>(s_rel, srow + k0 / 16 + 1);
     } else if (GK == 32) {
@@ -244,13 +257,22 @@ __device__ __forceinline__ void col_load(ColChunk<MB, SD, GK>& c, int first, int
 template <int MB, int SD, int GK>
 __device__ __forceinline__ void col_compute(const ColChunk<MB, SD, GK>& c, int first, int nst, int tw0,
                                             const float (&cbv)[16], bool cbf, uint32_t (&lut)[4], uint32_t (&lut2)[4],
-                                            v16i (&acc)[MB], int group) {
+                                            v16i (&acc)[MB], int group, const uint32_t* tab) {
 #pragma unroll
   for (int j = 0; j < kChunk; ++j) {
     const int i = first + j;
     if (i >= nst) break;  // uniform within the wavefront
     const int t = tw0 + i;
-    if (GK == 16) {
+    if (col_scale_table<SD, GK>()) {  // bytes of u8 loads: & 0xFF only states the table's bound
+      const u32x4 t1 = *reinterpret_cast<const u32x4*>(tab + (c.b1[j] & 0xFFu) * 4);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) lut[w] = t1[w];
+      if (GK == 16) {
+        const u32x4 t2 = *reinterpret_cast<const u32x4*>(tab + (c.b2[j] & 0xFFu) * 4);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) lut2[w] = t2[w];
+      }
+    } else if (GK == 16) {
       build_lut_fast(cbv, cbf, c.s1[j], lut);
       build_lut_fast(cbv, cbf, c.s2[j], lut2);
     } else if (GK == 32 || i == 0 || (t * kBK) % group == 0) {
@@ -287,6 +309,7 @@ __global__ __launch_bounds__(256) void gemm_w4_col_kernel(const int8_t* __restri
                                                           int64_t ldo, int odt, bool eager, int32_t* __restrict__ ws,
                                                           int32_t* __restrict__ acc_out) {
   __shared__ int32_t red[4][MB * 16][64];  // each wavefront's accumulators, register-major
+  __shared__ __attribute__((aligned(16))) uint32_t tab[col_scale_table<SD, GK>() ? 256 * 4 : 4];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar K-range bookkeeping
@@ -313,14 +336,20 @@ __global__ __launch_bounds__(256) void gemm_w4_col_kernel(const int8_t* __restri
 #pragma unroll
   for (int b = 0; b < MB; ++b) acc[b] = v16i{};
   uint32_t lut[4] = {0, 0, 0, 0}, lut2[4] = {0, 0, 0, 0};
+  if (col_scale_table<SD, GK>()) {  // 256 threads, one entry each; nothing returns before this barrier
+    uint32_t w4[4];
+    build_lut_fast(cbv, cbf, fp8e4m3fn_to_f32(static_cast<uint32_t>(tid)), w4);
+    *reinterpret_cast<u32x4*>(tab + tid * 4) = u32x4{w4[0], w4[1], w4[2], w4[3]};
+    __syncthreads();
+  }
 
   ColChunk<MB, SD, GK> c0, c1;
   if (nst > 0) col_load(c0, 0, nst, tw0, qrow, arow, s_rel, srow, kh, group);
   for (int first = 0; first < nst; first += 2 * kChunk) {
     if (first + kChunk < nst) col_load(c1, first + kChunk, nst, tw0, qrow, arow, s_rel, srow, kh, group);
-    col_compute(c0, first, nst, tw0, cbv, cbf, lut, lut2, acc, group);
+    col_compute(c0, first, nst, tw0, cbv, cbf, lut, lut2, acc, group, tab);
     if (first + 2 * kChunk < nst) col_load(c0, first + 2 * kChunk, nst, tw0, qrow, arow, s_rel, srow, kh, group);
-    col_compute(c1, first + kChunk, nst, tw0, cbv, cbf, lut, lut2, acc, group);
+    col_compute(c1, first + kChunk, nst, tw0, cbv, cbf, lut, lut2, acc, group, tab);
   }
 
 #pragma unroll
@@ -441,7 +470,13 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
     const void* __restrict__ s_rel, int64_t lds, const float* __restrict__ cb, int group, const float* __restrict__ sch,
     const void* __restrict__ bias, int M, int N, int K, int spw, void* __restrict__ out, int64_t ldo, int odt,
     bool eager, int32_t* __restrict__ acc_out) {
-  __shared__ __attribute__((aligned(1024))) int8_t smem[kC16MaxWaves * kWaveLds];
+  // fp8 scales with groups of 16 or 32 (a table per group, ~70 VALU each): the tables of all 256 scale bytes are
+  // built once per workgroup into 4 KiB of LDS (entry e = the 4 words of scale byte e), and a group's table is one
+  // 16-byte LDS read.  Same lut_word on the same operands: the same bytes as building it in place.
+  constexpr bool kTab = SD == H3K_FP8E4M3 && (GK == 16 || GK == 32);
+  constexpr int kTabBytes = kTab ? 256 * 16 : 0;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[kC16MaxWaves * kWaveLds + kTabBytes];
+  const int8_t* const tab = smem + kC16MaxWaves * kWaveLds;
   constexpr uint32_t sb = scale_bytes<SD>();
   constexpr int NS = GK == 16 ? 2 : 1;  // scales per lane, column and super-step
 
@@ -489,6 +524,17 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
   bool cbw_finite = true;
 #pragma unroll
   for (int i = 0; i < NCB; ++i) cbw_finite = cbw_finite && __builtin_isfinite(cbw[i]);
+  if (kTab) {
+    for (int e = tid; e < 256; e += static_cast<int>(blockDim.x)) {
+      const float s = scale_value<SD>(static_cast<uint32_t>(e));
+      const bool fast = cbw_finite && __builtin_isfinite(s);
+      uint32_t w4[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) w4[w] = lut_word(&cbw[4 * w], s, fast);
+      *reinterpret_cast<u32x4*>(smem + kC16MaxWaves * kWaveLds + e * 16) = u32x4{w4[0], w4[1], w4[2], w4[3]};
+    }
+    __syncthreads();  // every thread of the workgroup reaches it: nothing returns before the main loop
+  }
   // ds_bpermute byte addresses of the lanes that build the column's table words
   const uint32_t bp0 = GK >= 128 ? static_cast<uint32_t>(c16 * 4) : static_cast<uint32_t>((c16 + 16 * (g & 2)) * 4);
 
@@ -556,6 +602,15 @@ __global__ __launch_bounds__(64 * kC16MaxWaves) void gemm_w4_c16_kernel(
                                                                                   static_cast<int>(x0)));
               lut[cg][2 * h + 1] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(bp0 + 64 * h),
                                                                                       static_cast<int>(x1)));
+            }
+          } else if (kTab) {  // scale bytes are zero-extended u8 loads: & 0xFF only states the table's bound
+            const u32x4 t1 = *reinterpret_cast<const u32x4*>(tab + (scur[j][cg][0] & 0xFFu) * 16);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) lut[cg][w] = t1[w];
+            if (GK == 16) {
+              const u32x4 t2 = *reinterpret_cast<const u32x4*>(tab + (scur[j][cg][NS - 1] & 0xFFu) * 16);
+#pragma unroll
+              for (int w = 0; w < 4; ++w) lut2[cg][w] = t2[w];
             }
           } else {
 #pragma unroll

@@ -48,8 +48,13 @@ def run(m, n, k, group=128, kind="f16", mode="ck", odt=_lib.BF16, with_bias=Fals
     cb = (torch.linspace(-1, 1, 16) + 0.05 * torch.randn(16, generator=g)).float().numpy()
     if special:  # non-finite and zero codebook entries, infinite scales: NaN products must decode to 0
         cb[3], cb[5], cb[7], cb[8] = np.inf, -np.inf, np.nan, 0.0
-        s_raw[1, :] = np.inf
-        s_raw[2, 0] = -np.inf
+        if kind == "fp8":  # e4m3fn has no infinity: NaN bytes (both signs) and zero instead
+            s_raw[1, :] = 0x7F
+            s_raw[2, 0] = 0xFF
+            s_raw[3, :] = 0x00
+        else:
+            s_raw[1, :] = np.inf
+            s_raw[2, 0] = -np.inf
     xs = torch.rand(m, generator=g) * 1e-2 + 1e-4
     sch = torch.rand(n, generator=g) * 1e-2 + 1e-4
     tdt, name = ODT[odt]
@@ -121,8 +126,8 @@ def test_c16_every_row_group(m):
     run(m, C16_N, 1152, group=128, seed=100 + m)  # 9 super-steps over 8 wavefronts: uneven K split
 
 
-@pytest.mark.parametrize("group,kind", [(16, "fp8"), (32, "bf16"), (64, "f32"), (128, "f16"), (256, "fp8"),
-                                        (512, "f16"), (384, "bf16")])
+@pytest.mark.parametrize("group,kind", [(16, "fp8"), (32, "bf16"), (32, "fp8"), (64, "f32"), (128, "f16"),
+                                        (256, "fp8"), (512, "f16"), (384, "bf16")])
 def test_c16_groups_and_scale_kinds(group, kind):
     k = 1536 if group == 384 else 1024
     run(13, C16_N, k, group=group, kind=kind, seed=group + 1)
@@ -144,6 +149,16 @@ def test_c16_epilogue_variants(mode, odt):
 def test_c16_non_finite_codebook_and_scales(group):
     run(9, C16_N, 1024, group=group, kind="f32", seed=41, special=True)
     run(30, C16_N, 1024, group=group, kind="f32", seed=42, special=True)
+
+
+@pytest.mark.parametrize("group", [16, 32])
+def test_fp8_scale_table_with_non_finite_codebook(group):
+    """fp8 scales of groups 16 and 32 take their level tables from a per-workgroup table of all 256 scale bytes
+    (16-row and column kernels): non-finite codebook entries, NaN scale bytes of both signs and zero scales."""
+    run(9, C16_N, 1024, group=group, kind="fp8", seed=43, special=True)
+    run(16, C16_N, 5120, group=group, kind="fp8", seed=44, special=True)
+    run(30, C16_N, 5120, group=group, kind="fp8", seed=45, special=True)  # column kernel, one K split
+    run(20, 64, 1024, group=group, kind="fp8", seed=46, special=True)  # column kernel, K split over workgroups
 
 
 def test_rejects_what_it_does_not_cover():
