@@ -2,7 +2,8 @@
 //   w8[n, k] = clamp(rint_half_even(f32(codebook[nib(n, k)]) * f32(s_rel[n, k / group])), -127, 127)
 // nib(n, 2j) is the LOW nibble of q[n, j]; a NaN product (NaN scale byte) decodes to 0 like the reference's
 // nan_to_num'd pair table.  HBM-bound: each thread turns 8 packed bytes into 16 levels (one 16-byte store), or for
-// groups of 32 or more 32 levels through a 16-entry byte table per scale (decode_w4_lut_kernel).
+// groups of 32 or more 32 levels through a 16-entry byte table per scale (decode_w4_lut_kernel); fp8 scales of
+// other groups from 16 up read the tables of all 256 scale bytes from LDS (decode_w4_fp8tab_kernel).
 #include "h3k_w4.hpp"
 
 namespace h3k {
@@ -40,6 +41,48 @@ __global__ __launch_bounds__(256) void decode_w4_kernel(const uint8_t* __restric
     out[w4] = o;
   }
   *reinterpret_cast<uint4*>(w8 + row * ldw + c * 16) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// fp8 scales with groups of 16 (or odd multiples of 16), where a thread's 16 levels share one scale: an e4m3 scale
+// has 256 byte values, so the workgroup first builds the 16-entry table of every one (4 KiB of LDS, entry e byte i =
+// level(codebook[i], fp8(e)), the per-element function) and each of its threads then decodes kFp8TabReps chunks of
+// 16 levels, each through the table of its scale byte with byte permutes.  Consecutive threads take consecutive
+// chunks, so every pass of the workgroup loads 2 KiB and stores 4 KiB contiguous (within a row).
+constexpr int kFp8TabReps = 8;
+
+__global__ __launch_bounds__(256) void decode_w4_fp8tab_kernel(const uint8_t* __restrict__ q, int64_t ldq,
+                                                               const uint8_t* __restrict__ s_rel, int64_t lds,
+                                                               const float* __restrict__ cb, int64_t n, int k,
+                                                               int group, int8_t* __restrict__ w8, int64_t ldw) {
+  __shared__ __attribute__((aligned(16))) uint32_t tab[256 * 4];
+  {
+    const float s = fp8e4m3fn_to_f32(threadIdx.x);  // blockDim.x == 256: one entry per thread
+    uint32_t w4[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      w4[w] = level(cb[4 * w], s) | (level(cb[4 * w + 1], s) << 8) | (level(cb[4 * w + 2], s) << 16) |
+              (level(cb[4 * w + 3], s) << 24);
+    *reinterpret_cast<u32x4*>(tab + threadIdx.x * 4) = u32x4{w4[0], w4[1], w4[2], w4[3]};
+  }
+  __syncthreads();  // nothing returns before it
+  const int chunks = k >> 4;
+  const int64_t total = n * chunks;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * kFp8TabReps) + threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < kFp8TabReps; ++r) {
+    const int64_t t = base + r * 256;
+    if (t >= total) break;
+    const int64_t row = t / chunks;
+    const int c = static_cast<int>(t - row * chunks);
+    const uint2 pk = *reinterpret_cast<const uint2*>(q + row * ldq + c * 8);
+    const uint32_t sbyte = s_rel[row * lds + (c * 16) / group];  // a u8: the table index stays below 256
+    const u32x4 e = *reinterpret_cast<const u32x4*>(tab + sbyte * 4);
+    const uint32_t lut[4] = {e[0], e[1], e[2], e[3]};
+    uint32_t o0, o1, o2, o3;
+    lut_decode_word(lut, pk.x, o0, o1);
+    lut_decode_word(lut, pk.y, o2, o3);
+    *reinterpret_cast<uint4*>(w8 + row * ldw + c * 16) = make_uint4(o0, o1, o2, o3);
+  }
 }
 
 // Groups of 32 or more: a thread owns 32 consecutive levels of one row (16 packed bytes in, 32 bytes out, so a
@@ -190,6 +233,12 @@ static void launch_decode(const void* q, int64_t ldq, const void* s_rel, int64_t
     return;
   }
   const int64_t threads = n * (k / 16);
+  if (SD == H3K_FP8E4M3 && group >= 16) {
+    const dim3 g(static_cast<unsigned>((threads + 256 * kFp8TabReps - 1) / (256 * kFp8TabReps)));
+    hipLaunchKernelGGL(decode_w4_fp8tab_kernel, g, dim3(256), 0, st, static_cast<const uint8_t*>(q), ldq,
+                       static_cast<const uint8_t*>(s_rel), lds, cb, n, k, group, w8, ldw);
+    return;
+  }
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   if (group < 16)
     hipLaunchKernelGGL((decode_w4_kernel<SD, true>), grid, dim3(256), 0, st, static_cast<const uint8_t*>(q), ldq, s_rel,

@@ -370,11 +370,12 @@ def test_decode_ties_clamp_and_views_into_larger_buffers():
     assert torch.equal(ql.decode_int8_grid(sub), full)
 
 
-@pytest.mark.parametrize("group", [32, 64, 128, 256])
+@pytest.mark.parametrize("group", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("pad", [0, 8, 16])
 def test_decode_table_path_every_byte_nan_and_clamp_scales(group, pad):
-    """Groups of 32 or more decode through a per-scale byte table: every packed byte value, NaN / +-448 / zero /
-    negative fp8 scales, rows that are views with a 16-byte (table path) or 8-byte (per-element path) stride."""
+    """fp8 scales decode through byte tables (groups of 32 or more: one per scale, built in registers; groups of 16
+    and rows with an 8-byte stride: the workgroup's table of all 256 scale bytes): every packed byte value, NaN /
+    +-448 / zero / negative scales, rows that are views with a 16-byte or an 8-byte stride."""
     n, k = 24, 1024
     rng = np.random.default_rng(group + pad)
     q = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
