@@ -85,6 +85,40 @@ __global__ __launch_bounds__(256) void decode_w4_fp8tab_kernel(const uint8_t* __
   }
 }
 
+// The 4-word byte table of a scale that SH aligned lanes of a quad share (1, 2 or 4): lane j of the SH holds words
+// j * 4 / SH .. + 4 / SH; quad permutes hand every lane all four.  Every lane of the SH must be active.
+template <int SH>
+__device__ __forceinline__ void share_lut(const uint32_t (&mine)[4 / SH], uint32_t (&lut)[4]) {
+  if constexpr (SH == 1) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) lut[w] = mine[w];
+  } else if constexpr (SH == 2) {  // quad_perm [0,0,2,2] / [1,1,3,3]
+    lut[0] = __builtin_amdgcn_mov_dpp(mine[0], 0xA0, 0xF, 0xF, false);
+    lut[1] = __builtin_amdgcn_mov_dpp(mine[1], 0xA0, 0xF, 0xF, false);
+    lut[2] = __builtin_amdgcn_mov_dpp(mine[0], 0xF5, 0xF, 0xF, false);
+    lut[3] = __builtin_amdgcn_mov_dpp(mine[1], 0xF5, 0xF, 0xF, false);
+  } else {  // quad_perm [w,w,w,w]
+    lut[0] = __builtin_amdgcn_mov_dpp(mine[0], 0x00, 0xF, 0xF, false);
+    lut[1] = __builtin_amdgcn_mov_dpp(mine[0], 0x55, 0xF, 0xF, false);
+    lut[2] = __builtin_amdgcn_mov_dpp(mine[0], 0xAA, 0xF, 0xF, false);
+    lut[3] = __builtin_amdgcn_mov_dpp(mine[0], 0xFF, 0xF, 0xF, false);
+  }
+}
+
+// The SH-lane share of a scale's table: words j * 4 / SH .. of level(codebook[.], s).
+template <int SH>
+__device__ __forceinline__ void build_shared_lut(const float* __restrict__ cb, float s, int j, uint32_t (&lut)[4]) {
+  constexpr int NW = 4 / SH;
+  uint32_t mine[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int w = j * NW + i;
+    mine[i] = level(cb[4 * w], s) | (level(cb[4 * w + 1], s) << 8) | (level(cb[4 * w + 2], s) << 16) |
+              (level(cb[4 * w + 3], s) << 24);
+  }
+  share_lut<SH>(mine, lut);
+}
+
 // Groups of 32 or more: a thread owns 32 consecutive levels of one row (16 packed bytes in, 32 bytes out, so a
 // wavefront's loads and stores are contiguous) that share one scale.  The scale's 16 possible levels form a byte
 // table in 4 registers (byte c of word w = level(codebook[4w + c], s)); the SH lanes of a quad that share the
@@ -104,30 +138,8 @@ __global__ __launch_bounds__(256) void decode_w4_lut_kernel(const uint8_t* __res
   const int c = t - row * chunks;
   const u32x4 pk = *reinterpret_cast<const u32x4*>(q + static_cast<int64_t>(row) * ldq + c * 16);
   const float s = load_scale<SD>(s_rel, static_cast<int64_t>(row) * lds + (c * 32) / group);
-  constexpr int NW = 4 / SH;
-  const int j = t & (SH - 1);
-  uint32_t mine[NW];
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const int w = j * NW + i;
-    mine[i] = level(cb[4 * w], s) | (level(cb[4 * w + 1], s) << 8) | (level(cb[4 * w + 2], s) << 16) |
-              (level(cb[4 * w + 3], s) << 24);
-  }
   uint32_t lut[4];
-  if constexpr (SH == 1) {
-#pragma unroll
-    for (int w = 0; w < 4; ++w) lut[w] = mine[w];
-  } else if constexpr (SH == 2) {  // quad_perm [0,0,2,2] / [1,1,3,3]
-    lut[0] = __builtin_amdgcn_mov_dpp(mine[0], 0xA0, 0xF, 0xF, false);
-    lut[1] = __builtin_amdgcn_mov_dpp(mine[1], 0xA0, 0xF, 0xF, false);
-    lut[2] = __builtin_amdgcn_mov_dpp(mine[0], 0xF5, 0xF, 0xF, false);
-    lut[3] = __builtin_amdgcn_mov_dpp(mine[1], 0xF5, 0xF, 0xF, false);
-  } else {  // quad_perm [w,w,w,w]
-    lut[0] = __builtin_amdgcn_mov_dpp(mine[0], 0x00, 0xF, 0xF, false);
-    lut[1] = __builtin_amdgcn_mov_dpp(mine[0], 0x55, 0xF, 0xF, false);
-    lut[2] = __builtin_amdgcn_mov_dpp(mine[0], 0xAA, 0xF, 0xF, false);
-    lut[3] = __builtin_amdgcn_mov_dpp(mine[0], 0xFF, 0xF, 0xF, false);
-  }
+  build_shared_lut<SH>(cb, s, t & (SH - 1), lut);
   uint32_t o[8];
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -148,9 +160,13 @@ __global__ __launch_bounds__(256) void decode_w4_lut_kernel(const uint8_t* __res
 // one 32-row block: eight consecutive threads own a row's 128 packed bytes there, so every load instruction reads 8
 // whole 128-byte lines and every store writes 8 runs of 128 bytes (8 rows' 16 bytes, consecutive in a fragment).
 // Workgroups of one K-step each would split each line of the weight between workgroups far apart in time, and it
-// was fetched again.  Rows past n (the padding) are written as zeros.  GK: 0 for groups that are multiples of 32 (one scale per thread, its 16 levels as a byte table), 1 for
-// group 16 (two tables), 2 for groups 4 and 8 (levels computed per element).
-template <int SD, int GK>
+// was fetched again.  Rows past n (the padding) are written as zeros.  GK: 0 for groups that are multiples of 32
+// (one scale per thread, its 16 levels as a byte table; SH = 4 or 2 for groups that are multiples of 128 or 64,
+// where the quad's or pair's lanes, which hold k = 256T + 32j .. and so share a scale, each build 4 / SH words of
+// it and exchange them), 1 for group 16 (two tables), 2 for groups 4 and 8 (levels computed per element).  The
+// early returns below take whole sharing groups: a row's 8 lanes share its row, and with K a multiple of 128
+// (SH = 4) or the lanes of a pair sharing t (SH = 2) a group's lanes are past the last K-step together.
+template <int SD, int GK, int SH>
 __global__ __launch_bounds__(256) void decode_w4_packed_kernel(const uint8_t* __restrict__ q, int64_t ldq,
                                                                const void* __restrict__ s_rel, int64_t lds,
                                                                const float* __restrict__ cb, int n, int nbp,
@@ -185,6 +201,11 @@ __global__ __launch_bounds__(256) void decode_w4_packed_kernel(const uint8_t* __
       }
       o[w] = v;
     }
+  } else if (GK == 0 && SH > 1) {
+    uint32_t lut[4];
+    build_shared_lut<SH>(cb, load_scale<SD>(s_rel, srow + k0 / group), j & (SH - 1), lut);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) lut_decode_word(lut, pk[w], o[2 * w], o[2 * w + 1]);
   } else {
     float cbv[16];
 #pragma unroll
@@ -210,12 +231,15 @@ static void launch_decode_packed(const void* q, int64_t ldq, const void* s_rel, 
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(nbp) * ((kt + 3) / 4)));  // < 2^32 (host checks)
   const uint8_t* qb = static_cast<const uint8_t*>(q);
   const int nn = static_cast<int>(n);
-  if (group % 32 == 0)
-    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 0>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, kt);
-  else if (group == 16)
-    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 1>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, kt);
-  else
-    hipLaunchKernelGGL((decode_w4_packed_kernel<SD, 2>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp, group, wp, kt);
+#define H3K_DP(GK, SH)                                                                                              \
+  hipLaunchKernelGGL((decode_w4_packed_kernel<SD, GK, SH>), grid, dim3(256), 0, st, qb, ldq, s_rel, lds, cb, nn, nbp,  \
+                     group, wp, kt)
+  if (group % 128 == 0) H3K_DP(0, 4);
+  else if (group % 64 == 0) H3K_DP(0, 2);
+  else if (group % 32 == 0) H3K_DP(0, 1);
+  else if (group == 16) H3K_DP(1, 1);
+  else H3K_DP(2, 1);
+#undef H3K_DP
 }
 
 template <int SD>
