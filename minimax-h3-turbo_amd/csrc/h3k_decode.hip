@@ -171,6 +171,19 @@ __global__ __launch_bounds__(256) void decode_w4_packed_kernel(const uint8_t* __
                                                                const void* __restrict__ s_rel, int64_t lds,
                                                                const float* __restrict__ cb, int n, int nbp,
                                                                int group, int8_t* __restrict__ wp, int kt) {
+  // fp8 scales of group 16: the workgroup's table of all 256 scale bytes (entry e: build_lut_fast at fp8(e)), built
+  // before any thread returns; a thread's two tables are then two 16-byte LDS reads
+  constexpr bool kTab = SD == H3K_FP8E4M3 && GK == 1;
+  __shared__ __attribute__((aligned(16))) uint32_t tab[kTab ? 256 * 4 : 4];
+  if constexpr (kTab) {
+    float cbv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cbv[i] = cb[i];
+    uint32_t w4[4];
+    build_lut_fast(cbv, all_finite(cbv), fp8e4m3fn_to_f32(threadIdx.x), w4);  // blockDim.x == 256
+    *reinterpret_cast<u32x4*>(tab + threadIdx.x * 4) = u32x4{w4[0], w4[1], w4[2], w4[3]};
+    __syncthreads();
+  }
   const int b = static_cast<int>(blockIdx.x % static_cast<unsigned>(nbp));
   const int j = static_cast<int>(threadIdx.x & 7);  // 32-level chunk of the row within the 4 K-steps
   const int t = static_cast<int>(blockIdx.x / static_cast<unsigned>(nbp)) * 4 + (j >> 1);
@@ -200,6 +213,15 @@ __global__ __launch_bounds__(256) void decode_w4_packed_kernel(const uint8_t* __
         v |= level(cb[nib], load_scale<SD>(s_rel, srow + (k0 + i) / group)) << (8 * e);
       }
       o[w] = v;
+    }
+  } else if (kTab) {
+    const uint8_t* sbytes = static_cast<const uint8_t*>(s_rel) + srow + k0 / 16;  // u8: indexes stay below 256
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 e = *reinterpret_cast<const u32x4*>(tab + static_cast<uint32_t>(sbytes[h]) * 4);
+      const uint32_t lut[4] = {e[0], e[1], e[2], e[3]};
+      lut_decode_word(lut, pk[2 * h], o[4 * h], o[4 * h + 1]);
+      lut_decode_word(lut, pk[2 * h + 1], o[4 * h + 2], o[4 * h + 3]);
     }
   } else if (GK == 0 && SH > 1) {
     uint32_t lut[4];

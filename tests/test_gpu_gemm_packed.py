@@ -66,6 +66,24 @@ def test_packed_decode_is_the_packed_layout_of_the_oracle_grid(n, k, group, kind
     assert np.array_equal(pack(w8).cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("special", [False, True])
+def test_packed_decode_fp8_group16_every_scale_byte(special):
+    """fp8 scales of group 16 take their tables from the workgroup's table of all 256 scale bytes: every byte value
+    (NaN 0x7F / 0xFF, negatives, zero), with a finite codebook and with infinite / NaN codebook entries."""
+    n, k = 300, 512
+    rng = np.random.default_rng(7 + special)
+    q = rng.integers(0, 256, (n, k // 2), dtype=np.uint8).view(np.int8)
+    s = rng.integers(0, 256, (n, k // 16), dtype=np.uint8)
+    s.reshape(-1)[:256] = np.arange(256, dtype=np.uint8)
+    _, _, _, cb = gi.weight_fp8_g16(4, 64, seed=3)
+    if special:
+        cb[3], cb[5], cb[7], cb[8] = np.inf, -np.inf, np.nan, 0.0
+    from test_gpu_qlinear import make_w
+    w = make_w(q, s, "fp8", np.ones(n, np.float32), cb, 16, 64)
+    want = packed_from_rowmajor(ref.decode_int8_grid(q, s, "fp8", cb, 16))
+    assert np.array_equal(decode_packed(w).cpu().numpy(), want)
+
+
 def test_packed_layout_restatement_is_a_permutation_within_blocks():
     """The numpy restatement itself, against its defining formula element by element on a small grid."""
     n, k = 45, 128
