@@ -90,6 +90,43 @@ def synth_weight(n: int, k: int, dev, seed: int = 0, group: int = 128, convrot: 
     return q, s_rel, s_ch, cb
 
 
+def decode_packed_g16_fp8(dev, n: int = 13824, k: int = 5120, calls: int = 40) -> dict:
+    """The packed-grid decode of the checkpoint weight format (fp8 e4m3 relative scales per group of 16) at the
+    headline weight shape: random codes and finite scale bytes, codebook arange(-8, 8).  A bounded spin kernel ahead
+    of the loop lets the host enqueue every call first, so the event pair times the kernels alone."""
+    import torch
+
+    from h3turbo_amd import _lib
+
+    lib = _lib.load()
+    g = torch.Generator(device=dev).manual_seed(16)
+    q = torch.randint(0, 256, (n, k // 2), generator=g, device=dev, dtype=torch.uint8)
+    s = torch.randint(0, 0x7E, (n, k // 16), generator=g, device=dev, dtype=torch.uint8)  # no NaN bytes
+    cb = torch.arange(-8, 8, dtype=torch.float32, device=dev)
+    out = torch.empty(lib.h3k_w8_packed_bytes(n, k), dtype=torch.int8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    def call():
+        _lib.check(lib.h3k_decode_w4_packed(q.data_ptr(), k // 2, s.data_ptr(), _lib.FP8E4M3, k // 16, cb.data_ptr(), n,
+                                            k, 16, out.data_ptr(), sp), "decode packed g16")
+
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(4_000_000)  # a few ms of one spinning wavefront: the host gets ahead of the GPU
+    e0.record(stream)
+    for _ in range(calls):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / calls
+    nbytes = n * k // 2 + n * (k // 16) + (n + 255) // 256 * 256 * k
+    return {"n": n, "k": k, "group": 16, "scales": "fp8e4m3", "ms": round(ms, 4),
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def gemm_kernel_name(m: int, n: int, k: int, packed: bool, cus: int = 256) -> str:
     """The GEMM kernel the W4A8 linear runs for this shape with aligned operands: the packed-weight kernel where
     h3k_gemm_packed_serves accepts the shape, otherwise the rule of gemm_a8w8_launch (h3k_gemm.hip)."""
@@ -774,6 +811,7 @@ def main() -> None:
     }
     line["kernels"]["rotate_quant_config2"] = rotquant_config2(dev, rot=128)
     line["kernels"]["rotate_quant_config2_rot256"] = rotquant_config2(dev, rot=256)
+    line["kernels"]["decode_w4_packed_g16_fp8"] = decode_packed_g16_fp8(dev)
     if not args.no_block:
         del xq, w8, out
         line["block"] = block_measurement(dev, args.block_steps, max(1, args.warmup))
